@@ -1,0 +1,285 @@
+// Fused backward kernels for the elementwise family.
+//
+// The reference computes every gradient as a Python composition of forward
+// kernels, then adds it into the existing gradient with a separate in-place
+// kernel (src/nanotorch/autograd/ops_unary.py, ops_binary.py;
+// src/nanotorch/core.py:865-871).  Here one pass reads the upstream gradient,
+// the saved tensors and (in accumulate mode) the old gradient, and writes the
+// new gradient, evaluating the same fp32/fp64 rounding chain:
+//
+//   neg      g * -1                               ops_unary.py:32-33
+//   exp      g * y                                ops_unary.py:69-70
+//   log      g * pow(x, -1)      = g * (1 / x)    ops_unary.py:105-106
+//   sqrt     (g * 0.5) * pow(y, -1)               ops_unary.py:142-144
+//   tanh     g * (1 - pow(y, 2)) = g * (1 - y*y)  ops_unary.py:180-182
+//   sigmoid  (g * y) * (1 - y)                    ops_unary.py:218-220
+//   relu     g * float(y > 0)                     ops_unary.py:287-289
+//   pow      (g * e) * pow(x, e - 1)              ops_unary.py:264-266
+//   add      (g, g)                               ops_binary.py:49-50
+//   sub      (g, g * -1)                          ops_binary.py:95-100
+//   mul      (b * g, a * g)                       ops_binary.py:145-150
+//   div      (g / b, ((-a) / pow(b, 2)) * g)      ops_binary.py:197-202
+//
+// pow(v, -1) and pow(v, 2) are evaluated as 1 / v and v * v: both are what a
+// correctly rounded pow returns, and glibc's powf returns them bit for bit.
+// pow(x, e - 1) for a general e stays a pow call; e - 1 is formed in fp32
+// as the reference does with its fp32 exponent tensor.  Accumulate mode is
+// `old + term` with one rounding, the reference's add_inplace
+// (src/cpp/ops/inplace_ops.cu:75).
+#include "ew_engine.h"
+
+namespace nt {
+
+__device__ __forceinline__ float b_pow(float a, float e) { return powf(a, e); }
+__device__ __forceinline__ double b_pow(double a, double e) {
+  return pow(a, e);
+}
+
+template <int OP> constexpr bool unary_uses_saved() { return OP != NT_NEG; }
+
+template <int OP, class T, bool ACC> struct UnaryBwd {
+  T e;   // pow exponent (already rounded as the reference's fp32 tensor)
+  T em1; // e - 1 formed in fp32
+  static constexpr bool S = unary_uses_saved<OP>();
+  static constexpr int NI = 1 + (S ? 1 : 0) + (ACC ? 1 : 0);
+  __device__ __forceinline__ void operator()(const T (&x)[NI],
+                                             T (&y)[1]) const {
+    const T g = x[0];
+    const T s = S ? x[1] : T(0);
+    T t;
+    if constexpr (OP == NT_NEG)
+      t = g * T(-1);
+    else if constexpr (OP == NT_EXP)
+      t = g * s;
+    else if constexpr (OP == NT_LOG)
+      t = g * (T(1) / s);
+    else if constexpr (OP == NT_SQRT)
+      t = (g * T(0.5)) * (T(1) / s);
+    else if constexpr (OP == NT_TANH)
+      t = g * (T(1) - s * s);
+    else if constexpr (OP == NT_SIGMOID)
+      t = (g * s) * (T(1) - s);
+    else if constexpr (OP == NT_RELU)
+      t = g * (s > T(0) ? T(1) : T(0));
+    else
+      t = (g * e) * b_pow(s, em1);
+    if constexpr (ACC)
+      y[0] = x[NI - 1] + t;
+    else
+      y[0] = t;
+  }
+};
+
+// Gradients of a binary op.  NA / NB: which gradients are produced; AA / AB:
+// accumulate into them.  Inputs, in order: g, a (if read), b (if read),
+// ga_old (if NA && AA), gb_old (if NB && AB).
+template <int OP, class T, bool NA, bool NB, bool AA, bool AB>
+struct BinaryBwd {
+  static constexpr bool UA = (OP == NT_MUL || OP == NT_DIV) && NB;
+  static constexpr bool UB =
+      (OP == NT_MUL && NA) || (OP == NT_DIV && (NA || NB));
+  static constexpr int IA = 1;
+  static constexpr int IB = 1 + (UA ? 1 : 0);
+  static constexpr int IGA = IB + (UB ? 1 : 0);
+  static constexpr int IGB = IGA + ((NA && AA) ? 1 : 0);
+  static constexpr int NI = IGB + ((NB && AB) ? 1 : 0);
+  static constexpr int NO = (NA ? 1 : 0) + (NB ? 1 : 0);
+  __device__ __forceinline__ void operator()(const T (&x)[NI],
+                                             T (&y)[NO]) const {
+    const T g = x[0];
+    const T a = UA ? x[IA] : T(0);
+    const T b = UB ? x[IB] : T(0);
+    T ta = T(0), tb = T(0);
+    if constexpr (OP == NT_ADD) {
+      ta = g;
+      tb = g;
+    } else if constexpr (OP == NT_SUB) {
+      ta = g;
+      tb = g * T(-1);
+    } else if constexpr (OP == NT_MUL) {
+      ta = b * g;
+      tb = a * g;
+    } else {
+      if constexpr (NA)
+        ta = g / b;
+      if constexpr (NB)
+        tb = ((-a) / (b * b)) * g;
+    }
+    int o = 0;
+    if constexpr (NA) {
+      if constexpr (AA)
+        y[o] = x[IGA] + ta;
+      else
+        y[o] = ta;
+      ++o;
+    }
+    if constexpr (NB) {
+      if constexpr (AB)
+        y[o] = x[IGB] + tb;
+      else
+        y[o] = tb;
+    }
+  }
+};
+
+namespace {
+
+template <int OP, class T, bool ACC>
+void run_unary_bwd(const nt_view *g, const nt_view *s, double scalar,
+                   const nt_view *gx) {
+  using F = UnaryBwd<OP, T, ACC>;
+  const float ef = float(scalar);
+  F f{T(scalar), T(ef - 1.0f)};
+  const nt_view *ins[F::NI];
+  int k = 0;
+  ins[k++] = g;
+  if (F::S)
+    ins[k++] = s;
+  if (ACC)
+    ins[k++] = gx;
+  const nt_view *outs[1] = {gx};
+  launch_elementwise<T, T, F::NI, 1>(ins, outs, f);
+}
+
+template <int OP, class T>
+void unary_bwd_acc(const nt_view *g, const nt_view *s, double scalar,
+                   const nt_view *gx, bool acc) {
+  if (acc)
+    run_unary_bwd<OP, T, true>(g, s, scalar, gx);
+  else
+    run_unary_bwd<OP, T, false>(g, s, scalar, gx);
+}
+
+template <int OP, class T, bool NA, bool NB, bool AA, bool AB>
+void run_binary_bwd(const nt_view *g, const nt_view *a, const nt_view *b,
+                    const nt_view *ga, const nt_view *gb) {
+  using F = BinaryBwd<OP, T, NA, NB, AA, AB>;
+  const nt_view *ins[F::NI];
+  int k = 0;
+  ins[k++] = g;
+  if (F::UA)
+    ins[k++] = a;
+  if (F::UB)
+    ins[k++] = b;
+  if (NA && AA)
+    ins[k++] = ga;
+  if (NB && AB)
+    ins[k++] = gb;
+  const nt_view *outs[F::NO > 0 ? F::NO : 1];
+  int m = 0;
+  if (NA)
+    outs[m++] = ga;
+  if (NB)
+    outs[m++] = gb;
+  launch_elementwise<T, T, F::NI, F::NO>(ins, outs, F{});
+}
+
+template <int OP, class T>
+void binary_bwd_t(const nt_view *g, const nt_view *a, const nt_view *b,
+                  const nt_view *ga, bool aa, const nt_view *gb, bool ab) {
+  const bool na = ga != nullptr, nb = gb != nullptr;
+  if (na && nb) {
+    if (aa && ab)
+      run_binary_bwd<OP, T, true, true, true, true>(g, a, b, ga, gb);
+    else if (aa)
+      run_binary_bwd<OP, T, true, true, true, false>(g, a, b, ga, gb);
+    else if (ab)
+      run_binary_bwd<OP, T, true, true, false, true>(g, a, b, ga, gb);
+    else
+      run_binary_bwd<OP, T, true, true, false, false>(g, a, b, ga, gb);
+  } else if (na) {
+    if (aa)
+      run_binary_bwd<OP, T, true, false, true, false>(g, a, b, ga, gb);
+    else
+      run_binary_bwd<OP, T, true, false, false, false>(g, a, b, ga, gb);
+  } else if (nb) {
+    if (ab)
+      run_binary_bwd<OP, T, false, true, false, true>(g, a, b, ga, gb);
+    else
+      run_binary_bwd<OP, T, false, true, false, false>(g, a, b, ga, gb);
+  }
+}
+
+} // namespace
+} // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_unary_bwd(int32_t op, const nt_view *g, const nt_view *saved,
+                 double scalar, const nt_view *gx, int32_t accumulate) {
+  return guard([&] {
+    check_view(g, "unary_bwd");
+    check_view(gx, "unary_bwd");
+    require_same_shape(g, gx, "unary_bwd");
+    require_same_dtype(g, gx, "unary_bwd");
+    if (op != NT_NEG) {
+      check_view(saved, "unary_bwd");
+      require_same_shape(g, saved, "unary_bwd");
+      require_same_dtype(g, saved, "unary_bwd");
+    }
+    const bool acc = accumulate != 0;
+    dispatch_float(g->dtype, [&]<class T>() {
+      switch (op) {
+      case NT_NEG:
+        return unary_bwd_acc<NT_NEG, T>(g, saved, scalar, gx, acc);
+      case NT_EXP:
+        return unary_bwd_acc<NT_EXP, T>(g, saved, scalar, gx, acc);
+      case NT_LOG:
+        return unary_bwd_acc<NT_LOG, T>(g, saved, scalar, gx, acc);
+      case NT_SQRT:
+        return unary_bwd_acc<NT_SQRT, T>(g, saved, scalar, gx, acc);
+      case NT_TANH:
+        return unary_bwd_acc<NT_TANH, T>(g, saved, scalar, gx, acc);
+      case NT_SIGMOID:
+        return unary_bwd_acc<NT_SIGMOID, T>(g, saved, scalar, gx, acc);
+      case NT_RELU:
+        return unary_bwd_acc<NT_RELU, T>(g, saved, scalar, gx, acc);
+      case NT_POW:
+        return unary_bwd_acc<NT_POW, T>(g, saved, scalar, gx, acc);
+      }
+      fail(NT_ERR_VALUE, "unary_bwd: unknown op");
+    });
+  });
+}
+
+int nt_binary_bwd(int32_t op, const nt_view *g, const nt_view *a,
+                  const nt_view *b, const nt_view *ga, int32_t acc_a,
+                  const nt_view *gb, int32_t acc_b) {
+  return guard([&] {
+    check_view(g, "binary_bwd");
+    if (!ga && !gb)
+      return;
+    const bool reads_ab = (op == NT_MUL || op == NT_DIV);
+    if (reads_ab) {
+      check_view(a, "binary_bwd");
+      check_view(b, "binary_bwd");
+      require_same_shape(g, a, "binary_bwd");
+      require_same_shape(g, b, "binary_bwd");
+      require_same_dtype(g, a, "binary_bwd");
+      require_same_dtype(g, b, "binary_bwd");
+    }
+    for (const nt_view *v : {ga, gb})
+      if (v) {
+        check_view(v, "binary_bwd");
+        require_same_shape(g, v, "binary_bwd");
+        require_same_dtype(g, v, "binary_bwd");
+      }
+    dispatch_float(g->dtype, [&]<class T>() {
+      switch (op) {
+      case NT_ADD:
+        return binary_bwd_t<NT_ADD, T>(g, a, b, ga, acc_a, gb, acc_b);
+      case NT_SUB:
+        return binary_bwd_t<NT_SUB, T>(g, a, b, ga, acc_a, gb, acc_b);
+      case NT_MUL:
+        return binary_bwd_t<NT_MUL, T>(g, a, b, ga, acc_a, gb, acc_b);
+      case NT_DIV:
+        return binary_bwd_t<NT_DIV, T>(g, a, b, ga, acc_a, gb, acc_b);
+      }
+      fail(NT_ERR_VALUE, "binary_bwd: unknown op");
+    });
+  });
+}
+
+} // extern "C"

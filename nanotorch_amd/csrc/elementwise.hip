@@ -1,0 +1,326 @@
+// Forward elementwise ops: unary (exp/log/neg/relu/sqrt/tanh/sigmoid/pow),
+// binary (add/sub/mul/div and the ==, >, >= comparisons), in-place updates,
+// casts/strided copies and whole-tensor equality.  All run through the
+// elementwise engine (ew_engine.h).
+//
+// Arithmetic follows the reference's functors exactly:
+//   src/cpp/ops/unary_ops.cu:40-58 (int_pow / PowOp), :101-107 (unary)
+//   src/cpp/ops/binary_ops.cu:107-113 (binary and comparisons)
+//   src/cpp/ops/inplace_ops.cu:75-79 (in-place)
+//   src/cpp/storage.cpp:55-61 (casts: bool is s != 0, else static_cast)
+// fp32 division and square root are correctly rounded
+// (-fhip-fp32-correctly-rounded-divide-sqrt) and nothing is contracted into
+// FMA (-ffp-contract=off), so +,-,*,/,sqrt match the host bit for bit.
+#include "ew_engine.h"
+
+namespace nt {
+
+// --------------------------------------------------------- device math
+
+__device__ __forceinline__ float d_exp(float a) { return expf(a); }
+__device__ __forceinline__ double d_exp(double a) { return exp(a); }
+__device__ __forceinline__ float d_log(float a) { return logf(a); }
+__device__ __forceinline__ double d_log(double a) { return log(a); }
+__device__ __forceinline__ float d_sqrt(float a) { return sqrtf(a); }
+__device__ __forceinline__ double d_sqrt(double a) { return sqrt(a); }
+__device__ __forceinline__ float d_tanh(float a) { return tanhf(a); }
+__device__ __forceinline__ double d_tanh(double a) { return tanh(a); }
+__device__ __forceinline__ float d_pow(float a, float e) { return powf(a, e); }
+__device__ __forceinline__ double d_pow(double a, double e) {
+  return pow(a, e);
+}
+
+// Square-and-multiply for integer dtypes (reference: int_pow,
+// src/cpp/ops/unary_ops.cu:40-49).
+template <class T> __device__ __forceinline__ T int_pow(T a, T n) {
+  T r = 1;
+  while (n > 0) {
+    if (n & 1)
+      r *= a;
+    a *= a;
+    n >>= 1;
+  }
+  return r;
+}
+
+// ------------------------------------------------------------ functors
+
+template <int OP, class T> struct UnaryFwd {
+  T e; // exponent for NT_POW, as the reference's value.item<T>()
+  __device__ __forceinline__ void operator()(const T (&x)[1], T (&y)[1]) const {
+    const T a = x[0];
+    if constexpr (OP == NT_EXP)
+      y[0] = d_exp(a);
+    else if constexpr (OP == NT_LOG)
+      y[0] = d_log(a);
+    else if constexpr (OP == NT_NEG)
+      y[0] = -a;
+    else if constexpr (OP == NT_RELU)
+      y[0] = (a >= 0) ? a : T(0);
+    else if constexpr (OP == NT_SQRT)
+      y[0] = d_sqrt(a);
+    else if constexpr (OP == NT_TANH)
+      y[0] = d_tanh(a);
+    else if constexpr (OP == NT_SIGMOID)
+      y[0] = T(1) / (T(1) + d_exp(-a));
+    else if constexpr (OP == NT_POW) {
+      if constexpr (std::is_integral_v<T>)
+        y[0] = int_pow(a, e);
+      else
+        y[0] = d_pow(a, e);
+    }
+  }
+};
+
+template <int OP, class T> struct BinaryFwd {
+  __device__ __forceinline__ void operator()(const T (&x)[2], T (&y)[1]) const {
+    const T a = x[0], b = x[1];
+    if constexpr (OP == NT_ADD)
+      y[0] = a + b;
+    else if constexpr (OP == NT_SUB)
+      y[0] = a - b;
+    else if constexpr (OP == NT_MUL)
+      y[0] = a * b;
+    else if constexpr (OP == NT_DIV)
+      y[0] = a / b;
+  }
+};
+
+template <int OP, class T> struct CompareFwd {
+  __device__ __forceinline__ void operator()(const T (&x)[2],
+                                             bool (&y)[1]) const {
+    if constexpr (OP == NT_EQ)
+      y[0] = x[0] == x[1];
+    else if constexpr (OP == NT_GT)
+      y[0] = x[0] > x[1];
+    else
+      y[0] = x[0] >= x[1];
+  }
+};
+
+template <class TI, class TO> struct CastOp {
+  __device__ __forceinline__ void operator()(const TI (&x)[1],
+                                             TO (&y)[1]) const {
+    if constexpr (std::is_same_v<TO, bool>)
+      y[0] = (x[0] != TI(0));
+    else
+      y[0] = static_cast<TO>(x[0]);
+  }
+};
+
+// ------------------------------------------------------------ host side
+
+namespace {
+
+template <int OP, class T> void run_unary(const nt_view *x, double scalar,
+                                          const nt_view *out) {
+  UnaryFwd<OP, T> f{static_cast<T>(scalar)};
+  const nt_view *ins[1] = {x};
+  const nt_view *outs[1] = {out};
+  launch_elementwise<T, T, 1, 1>(ins, outs, f);
+}
+
+template <int OP> void unary_float(const nt_view *x, double s,
+                                   const nt_view *out) {
+  dispatch_float(x->dtype, [&]<class T>() { run_unary<OP, T>(x, s, out); });
+}
+
+template <int OP> void unary_arith(const nt_view *x, double s,
+                                   const nt_view *out) {
+  dispatch_arith(x->dtype, [&]<class T>() { run_unary<OP, T>(x, s, out); });
+}
+
+template <int OP> void binary_all(const nt_view *a, const nt_view *b,
+                                  const nt_view *out) {
+  dispatch_all(a->dtype, [&]<class T>() {
+    const nt_view *ins[2] = {a, b};
+    const nt_view *outs[1] = {out};
+    launch_elementwise<T, T, 2, 1>(ins, outs, BinaryFwd<OP, T>{});
+  });
+}
+
+template <int OP> void binary_arith(const nt_view *a, const nt_view *b,
+                                    const nt_view *out) {
+  dispatch_arith(a->dtype, [&]<class T>() {
+    const nt_view *ins[2] = {a, b};
+    const nt_view *outs[1] = {out};
+    launch_elementwise<T, T, 2, 1>(ins, outs, BinaryFwd<OP, T>{});
+  });
+}
+
+template <int OP> void compare_all(const nt_view *a, const nt_view *b,
+                                   const nt_view *out) {
+  dispatch_all(a->dtype, [&]<class T>() {
+    const nt_view *ins[2] = {a, b};
+    const nt_view *outs[1] = {out};
+    launch_elementwise<T, bool, 2, 1>(ins, outs, CompareFwd<OP, T>{});
+  });
+}
+
+void binary_dispatch(int op, const nt_view *a, const nt_view *b,
+                     const nt_view *out, const char *fname) {
+  check_view(a, fname);
+  check_view(b, fname);
+  check_view(out, fname);
+  require_same_shape(a, b, fname);
+  require_same_shape(a, out, fname);
+  require_same_dtype(a, b, fname);
+  const bool cmp = (op == NT_EQ || op == NT_GT || op == NT_GE);
+  if (cmp ? out->dtype != NT_BOOL : out->dtype != a->dtype)
+    fail(NT_ERR_RUNTIME, std::string(fname) + ": output dtype mismatch");
+  switch (op) {
+  case NT_ADD:
+    return binary_all<NT_ADD>(a, b, out);
+  case NT_SUB:
+    return binary_all<NT_SUB>(a, b, out);
+  case NT_MUL:
+    return binary_all<NT_MUL>(a, b, out);
+  case NT_DIV:
+    return binary_arith<NT_DIV>(a, b, out);
+  case NT_EQ:
+    return compare_all<NT_EQ>(a, b, out);
+  case NT_GT:
+    return compare_all<NT_GT>(a, b, out);
+  case NT_GE:
+    return compare_all<NT_GE>(a, b, out);
+  }
+  fail(NT_ERR_VALUE, std::string(fname) + ": unknown op");
+}
+
+template <class T> struct NotEqualFlag {
+  __device__ __forceinline__ void operator()(const T (&x)[2],
+                                             bool (&y)[1]) const {
+    y[0] = !(x[0] == x[1]);
+  }
+};
+
+__global__ void any_true_kernel(const bool *v, int64_t n, int *flag) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  bool any = false;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride)
+    any |= v[i];
+  if (any)
+    atomicOr(flag, 1);
+}
+
+} // namespace
+} // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_copy(const nt_view *src, const nt_view *dst) {
+  return guard([&] {
+    check_view(src, "copy");
+    check_view(dst, "copy");
+    require_same_shape(src, dst, "copy");
+    dispatch_all(src->dtype, [&]<class TI>() {
+      dispatch_all(dst->dtype, [&]<class TO>() {
+        const nt_view *ins[1] = {src};
+        const nt_view *outs[1] = {dst};
+        launch_elementwise<TI, TO, 1, 1>(ins, outs, CastOp<TI, TO>{});
+      });
+    });
+  });
+}
+
+int nt_unary(int32_t op, const nt_view *x, double scalar, const nt_view *out) {
+  return guard([&] {
+    check_view(x, "unary");
+    check_view(out, "unary");
+    require_same_shape(x, out, "unary");
+    require_same_dtype(x, out, "unary");
+    switch (op) {
+    case NT_EXP:
+      return unary_float<NT_EXP>(x, scalar, out);
+    case NT_LOG:
+      return unary_float<NT_LOG>(x, scalar, out);
+    case NT_NEG:
+      return unary_arith<NT_NEG>(x, scalar, out);
+    case NT_RELU:
+      return unary_arith<NT_RELU>(x, scalar, out);
+    case NT_SQRT:
+      return unary_float<NT_SQRT>(x, scalar, out);
+    case NT_TANH:
+      return unary_float<NT_TANH>(x, scalar, out);
+    case NT_SIGMOID:
+      return unary_float<NT_SIGMOID>(x, scalar, out);
+    case NT_POW:
+      return unary_arith<NT_POW>(x, scalar, out);
+    }
+    fail(NT_ERR_VALUE, "unary: unknown op");
+  });
+}
+
+int nt_binary(int32_t op, const nt_view *a, const nt_view *b,
+              const nt_view *out) {
+  return guard([&] { binary_dispatch(op, a, b, out, "_dispatch_binary"); });
+}
+
+int nt_inplace(int32_t op, const nt_view *out, const nt_view *other) {
+  return guard([&] {
+    check_view(out, "_dispatch_inplace_apply");
+    check_view(other, "_dispatch_inplace_apply");
+    require_same_dtype(out, other, "_dispatch_inplace_apply");
+    require_same_shape(out, other, "_dispatch_inplace_apply");
+    if (op == NT_COPY) {
+      dispatch_all(out->dtype, [&]<class T>() {
+        const nt_view *ins[1] = {other};
+        const nt_view *outs[1] = {out};
+        launch_elementwise<T, T, 1, 1>(ins, outs, CastOp<T, T>{});
+      });
+      return;
+    }
+    if (op != NT_ADD && op != NT_SUB && op != NT_MUL && op != NT_DIV)
+      fail(NT_ERR_VALUE, "inplace: unknown op");
+    binary_dispatch(op, out, other, out, "_dispatch_inplace_apply");
+  });
+}
+
+int nt_equals(const nt_view *a, const nt_view *b, int32_t *result) {
+  return guard([&] {
+    check_view(a, "equals");
+    check_view(b, "equals");
+    require_same_shape(a, b, "equals");
+    require_same_dtype(a, b, "equals");
+    const int64_t n = numel(a);
+    if (n == 0) {
+      *result = 1;
+      return;
+    }
+    // Materialise a != b as a bool mask, then OR-reduce it into a flag.
+    void *mask = device_alloc(size_t(n));
+    void *flag = device_alloc(sizeof(int));
+    nt_view mv{};
+    mv.data = mask;
+    mv.dtype = NT_BOOL;
+    mv.ndim = a->ndim;
+    int64_t st = 1;
+    for (int d = a->ndim - 1; d >= 0; --d) {
+      mv.shape[d] = a->shape[d];
+      mv.strides[d] = st;
+      st *= a->shape[d];
+    }
+    dispatch_all(a->dtype, [&]<class T>() {
+      const nt_view *ins[2] = {a, b};
+      const nt_view *outs[1] = {&mv};
+      launch_elementwise<T, bool, 2, 1>(ins, outs, NotEqualFlag<T>{});
+    });
+    NT_HIP_CHECK(hipMemsetAsync(flag, 0, sizeof(int), stream()));
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    any_true_kernel<<<dim3(unsigned(blocks)), 256, 0, stream()>>>(
+        static_cast<const bool *>(mask), n, static_cast<int *>(flag));
+    NT_LAUNCH_CHECK();
+    int host_flag = 0;
+    NT_HIP_CHECK(hipMemcpyAsync(&host_flag, flag, sizeof(int),
+                                hipMemcpyDeviceToHost, stream()));
+    NT_HIP_CHECK(hipStreamSynchronize(stream()));
+    device_free(mask);
+    device_free(flag);
+    *result = host_flag ? 0 : 1;
+  });
+}
+
+} // extern "C"

@@ -1,0 +1,410 @@
+// Elementwise engine: one launcher that runs a device functor over NI input
+// and NO output views of one logical shape, picking among three kernels:
+//
+//  * flat    -- every operand is contiguous in the same logical order (or a
+//               broadcast scalar).  Each thread moves UNROLL vectors of 16 B
+//               per operand (dwordx4 loads/stores), which is what an
+//               HBM-bound op needs on CDNA.
+//  * tile2d  -- after merging dims, the iteration space is 2-D.  A 64x64 tile
+//               per workgroup; operands whose rows are contiguous are read
+//               straight (a wave reads 64 consecutive elements); operands
+//               that are contiguous along the other axis (e.g. `x.T`) are
+//               staged through a padded LDS tile so both the global read and
+//               the global write stay coalesced.  Outputs laid out that way
+//               go back through the same LDS tile.
+//  * generic -- anything else (up to 8 dims): per-element unravel with
+//               multiply-high division when the index fits in 32 bits.
+//
+// The reference has one thread per element and a 64-bit div/mod per dim per
+// element for every non-contiguous view (src/cpp/tensor_view.cuh:42-84,
+// src/cpp/ops/unary_ops.cu:19-26, binary_ops.cu:22-41).
+//
+// Functor contract: `void operator()(const TI (&x)[NI], TO (&y)[NO]) const`,
+// __device__, trivially copyable.  Each element's inputs are read before its
+// outputs are written by the same work-item (flat/generic) or workgroup
+// (tile2d), so an output may be the same view as an input (in-place ops and
+// gradient accumulation).
+#pragma once
+
+#include <algorithm>
+
+#include "nt_internal.h"
+
+namespace nt {
+
+constexpr int EW_THREADS = 256;
+constexpr int EW_TILE = 64;
+constexpr int EW_TILE_PAD = 65;
+
+template <class T, int N> struct PtrPack {
+  T *p[N > 0 ? N : 1];
+};
+
+template <class T, int VEC> struct alignas(sizeof(T) * VEC) VecT {
+  T v[VEC];
+};
+
+template <int N> struct Strides2 {
+  int64_t r[N > 0 ? N : 1];
+  int64_t c[N > 0 ? N : 1];
+};
+
+template <int N> struct StridesN {
+  int64_t s[N][NT_MAX_DIMS];
+};
+
+struct ShapeN {
+  int ndim;
+  int64_t shape[NT_MAX_DIMS];
+  FastDivU32 fd[NT_MAX_DIMS];
+};
+
+// ------------------------------------------------------------------- flat
+
+template <class TI, class TO, int NI, int NO, int VEC, int UNROLL, class F>
+__global__ __launch_bounds__(EW_THREADS) void ew_flat_kernel(
+    PtrPack<const TI, NI> in, uint32_t scalar_mask, PtrPack<TO, NO> out,
+    int64_t nvec, int64_t n, F f) {
+  using VI = VecT<TI, VEC>;
+  using VO = VecT<TO, VEC>;
+  const int64_t base =
+      int64_t(blockIdx.x) * (EW_THREADS * UNROLL) + threadIdx.x;
+  VI a[UNROLL][NI > 0 ? NI : 1];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t vi = base + int64_t(u) * EW_THREADS;
+    if (vi < nvec) {
+#pragma unroll
+      for (int k = 0; k < NI; ++k) {
+        if (scalar_mask & (1u << k)) {
+          const TI s = in.p[k][0];
+#pragma unroll
+          for (int j = 0; j < VEC; ++j)
+            a[u][k].v[j] = s;
+        } else {
+          a[u][k] = reinterpret_cast<const VI *>(in.p[k])[vi];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t vi = base + int64_t(u) * EW_THREADS;
+    if (vi < nvec) {
+      VO o[NO];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        TI x[NI > 0 ? NI : 1];
+        TO y[NO];
+#pragma unroll
+        for (int k = 0; k < NI; ++k)
+          x[k] = a[u][k].v[j];
+        f(x, y);
+#pragma unroll
+        for (int m = 0; m < NO; ++m)
+          o[m].v[j] = y[m];
+      }
+#pragma unroll
+      for (int m = 0; m < NO; ++m)
+        reinterpret_cast<VO *>(out.p[m])[vi] = o[m];
+    }
+  }
+  // Fewer than VEC trailing elements: block 0 takes them one per thread.
+  const int64_t tail0 = nvec * VEC;
+  if (blockIdx.x == 0 && int64_t(threadIdx.x) < n - tail0) {
+    const int64_t i = tail0 + threadIdx.x;
+    TI x[NI > 0 ? NI : 1];
+    TO y[NO];
+#pragma unroll
+    for (int k = 0; k < NI; ++k)
+      x[k] = in.p[k][(scalar_mask & (1u << k)) ? 0 : i];
+    f(x, y);
+#pragma unroll
+    for (int m = 0; m < NO; ++m)
+      out.p[m][i] = y[m];
+  }
+}
+
+// ----------------------------------------------------------------- tile2d
+
+template <class TI, class TO, int NI, int NO, class F>
+__global__ __launch_bounds__(EW_THREADS) void ew_tile_kernel(
+    PtrPack<const TI, NI> in, Strides2<NI> sin, uint32_t col_in,
+    PtrPack<TO, NO> out, Strides2<NO> sout, uint32_t col_out, int64_t R,
+    int64_t C, int64_t tiles_c, F f) {
+  constexpr int T = EW_TILE, P = EW_TILE_PAD;
+  constexpr size_t LB = sizeof(TI) > sizeof(TO) ? sizeof(TI) : sizeof(TO);
+  __shared__ __align__(16) unsigned char lds_raw[T * P * LB];
+  const int tx = threadIdx.x & (T - 1);
+  const int ty = threadIdx.x >> 6; // 0..3
+  const int64_t tr = int64_t(blockIdx.x) / tiles_c;
+  const int64_t tc = int64_t(blockIdx.x) - tr * tiles_c;
+  const int64_t r0 = tr * T, c0 = tc * T;
+  constexpr int EPT = T * T / EW_THREADS; // 16 elements per thread
+
+  // Work-item (tx, ty) owns tile elements (row ty + 4j, col tx), j < 16.
+  TI v[NI > 0 ? NI : 1][EPT];
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    const TI *p = in.p[k];
+    const int64_t sr = sin.r[k], sc = sin.c[k];
+    if (col_in & (1u << k)) {
+      // Rows are contiguous in memory along the tile's row index: lanes
+      // walk rows, the tile is stored column-major in LDS, then read back
+      // in the owner layout.
+      TI *lds = reinterpret_cast<TI *>(lds_raw);
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int cl = ty + 4 * j;
+        const int64_t r = r0 + tx, c = c0 + cl;
+        if (r < R && c < C)
+          lds[cl * P + tx] = p[r * sr + c * sc];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < EPT; ++j)
+        v[k][j] = lds[tx * P + ty + 4 * j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int64_t r = r0 + ty + 4 * j, c = c0 + tx;
+        v[k][j] = (r < R && c < C) ? p[r * sr + c * sc] : TI(0);
+      }
+    }
+  }
+  TO o[NO][EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    TI x[NI > 0 ? NI : 1];
+    TO y[NO];
+#pragma unroll
+    for (int k = 0; k < NI; ++k)
+      x[k] = v[k][j];
+    f(x, y);
+#pragma unroll
+    for (int m = 0; m < NO; ++m)
+      o[m][j] = y[m];
+  }
+#pragma unroll
+  for (int m = 0; m < NO; ++m) {
+    TO *p = out.p[m];
+    const int64_t sr = sout.r[m], sc = sout.c[m];
+    if (col_out & (1u << m)) {
+      TO *lds = reinterpret_cast<TO *>(lds_raw);
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < EPT; ++j)
+        lds[tx * P + ty + 4 * j] = o[m][j];
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int cl = ty + 4 * j;
+        const int64_t r = r0 + tx, c = c0 + cl;
+        if (r < R && c < C)
+          p[r * sr + c * sc] = lds[cl * P + tx];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const int64_t r = r0 + ty + 4 * j, c = c0 + tx;
+        if (r < R && c < C)
+          p[r * sr + c * sc] = o[m][j];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- generic
+
+template <class TI, class TO, int NI, int NO, bool IDX32, class F>
+__global__ __launch_bounds__(EW_THREADS) void ew_generic_kernel(
+    PtrPack<const TI, NI> in, PtrPack<TO, NO> out, StridesN<NI + NO> st,
+    ShapeN sh, int64_t n, F f) {
+  const int64_t stride = int64_t(gridDim.x) * EW_THREADS;
+  for (int64_t i = int64_t(blockIdx.x) * EW_THREADS + threadIdx.x; i < n;
+       i += stride) {
+    int64_t off[NI + NO];
+#pragma unroll
+    for (int k = 0; k < NI + NO; ++k)
+      off[k] = 0;
+    if constexpr (IDX32) {
+      uint32_t rem = uint32_t(i);
+#pragma unroll
+      for (int d = NT_MAX_DIMS - 1; d >= 0; --d) {
+        if (d < sh.ndim) {
+          const uint32_t q = sh.fd[d].div(rem);
+          const int64_t coord = int64_t(rem - q * uint32_t(sh.shape[d]));
+          rem = q;
+#pragma unroll
+          for (int k = 0; k < NI + NO; ++k)
+            off[k] += coord * st.s[k][d];
+        }
+      }
+    } else {
+      int64_t rem = i;
+#pragma unroll
+      for (int d = NT_MAX_DIMS - 1; d >= 0; --d) {
+        if (d < sh.ndim) {
+          const int64_t q = rem / sh.shape[d];
+          const int64_t coord = rem - q * sh.shape[d];
+          rem = q;
+#pragma unroll
+          for (int k = 0; k < NI + NO; ++k)
+            off[k] += coord * st.s[k][d];
+        }
+      }
+    }
+    TI x[NI > 0 ? NI : 1];
+    TO y[NO];
+#pragma unroll
+    for (int k = 0; k < NI; ++k)
+      x[k] = in.p[k][off[k]];
+    f(x, y);
+#pragma unroll
+    for (int m = 0; m < NO; ++m)
+      out.p[m][off[NI + m]] = y[m];
+  }
+}
+
+// ---------------------------------------------------------------- launcher
+
+template <class T> constexpr int ew_vec() {
+  return sizeof(T) >= 16 ? 1 : int(16 / sizeof(T));
+}
+
+template <class TI, class TO, int NI, int NO, class F>
+void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
+                        F f) {
+  constexpr int NT = NI + NO;
+  const nt_view *all[NT];
+  for (int k = 0; k < NI; ++k)
+    all[k] = ins[k];
+  for (int m = 0; m < NO; ++m)
+    all[NI + m] = outs[m];
+  const int64_t n = numel(outs[0]);
+  if (n == 0)
+    return;
+
+  PtrPack<const TI, NI> pin{};
+  PtrPack<TO, NO> pout{};
+  for (int k = 0; k < NI; ++k)
+    pin.p[k] = typed_ptr<const TI>(ins[k]);
+  for (int m = 0; m < NO; ++m)
+    pout.p[m] = typed_ptr<TO>(outs[m]);
+
+  JointLayout L = coalesce(all, NT);
+  hipStream_t s = stream();
+
+  // ---- flat: every operand unit-stride (inputs may be stride-0 scalars).
+  bool flat = L.ndim <= 1;
+  uint32_t smask = 0;
+  if (L.ndim == 0) {
+    smask = (1u << NI) - 1;
+  } else if (flat) {
+    for (int k = 0; k < NT && flat; ++k) {
+      const int64_t st = L.strides[k][0];
+      if (st == 1)
+        continue;
+      if (st == 0 && k < NI)
+        smask |= 1u << k;
+      else
+        flat = false;
+    }
+  }
+  if (flat) {
+    constexpr int VBIG = ew_vec<TI>() < ew_vec<TO>() ? ew_vec<TI>()
+                                                      : ew_vec<TO>();
+    constexpr int UNROLL = 4;
+    bool aligned = true;
+    for (int k = 0; k < NI; ++k)
+      if (!(smask & (1u << k)) &&
+          reinterpret_cast<uintptr_t>(pin.p[k]) % (sizeof(TI) * VBIG) != 0)
+        aligned = false;
+    for (int m = 0; m < NO; ++m)
+      if (reinterpret_cast<uintptr_t>(pout.p[m]) % (sizeof(TO) * VBIG) != 0)
+        aligned = false;
+    if (aligned) {
+      const int64_t nvec = n / VBIG;
+      const int64_t blocks =
+          std::max<int64_t>(1, (nvec + EW_THREADS * UNROLL - 1) /
+                                   (EW_THREADS * UNROLL));
+      ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, F>
+          <<<dim3(unsigned(blocks)), EW_THREADS, 0, s>>>(pin, smask, pout,
+                                                          nvec, n, f);
+    } else {
+      const int64_t blocks = std::max<int64_t>(
+          1, (n + EW_THREADS * UNROLL - 1) / (EW_THREADS * UNROLL));
+      ew_flat_kernel<TI, TO, NI, NO, 1, UNROLL, F>
+          <<<dim3(unsigned(blocks)), EW_THREADS, 0, s>>>(pin, smask, pout, n,
+                                                          n, f);
+    }
+    NT_LAUNCH_CHECK();
+    return;
+  }
+
+  // ---- tile2d
+  if (L.ndim == 2) {
+    Strides2<NI> sin{};
+    Strides2<NO> sout{};
+    uint32_t col_in = 0, col_out = 0;
+    for (int k = 0; k < NI; ++k) {
+      sin.r[k] = L.strides[k][0];
+      sin.c[k] = L.strides[k][1];
+      if (sin.r[k] == 1 && sin.c[k] != 1)
+        col_in |= 1u << k;
+    }
+    for (int m = 0; m < NO; ++m) {
+      sout.r[m] = L.strides[NI + m][0];
+      sout.c[m] = L.strides[NI + m][1];
+      if (sout.r[m] == 1 && sout.c[m] != 1)
+        col_out |= 1u << m;
+    }
+    const int64_t R = L.shape[0], C = L.shape[1];
+    const int64_t tiles_r = (R + EW_TILE - 1) / EW_TILE;
+    const int64_t tiles_c = (C + EW_TILE - 1) / EW_TILE;
+    const int64_t blocks = tiles_r * tiles_c;
+    if (blocks < (int64_t(1) << 31)) {
+      ew_tile_kernel<TI, TO, NI, NO, F>
+          <<<dim3(unsigned(blocks)), EW_THREADS, 0, s>>>(
+              pin, sin, col_in, pout, sout, col_out, R, C, tiles_c, f);
+      NT_LAUNCH_CHECK();
+      return;
+    }
+  }
+
+  // ---- generic
+  StridesN<NT> st{};
+  ShapeN sh{};
+  sh.ndim = L.ndim;
+  for (int d = 0; d < L.ndim; ++d) {
+    sh.shape[d] = L.shape[d];
+    for (int k = 0; k < NT; ++k)
+      st.s[k][d] = L.strides[k][d];
+  }
+  const bool idx32 = n < (int64_t(1) << 32);
+  if (idx32)
+    for (int d = 0; d < L.ndim; ++d)
+      sh.fd[d] = FastDivU32(uint32_t(L.shape[d]));
+  const int64_t want = (n + EW_THREADS * 4 - 1) / (EW_THREADS * 4);
+  const int64_t blocks =
+      std::max<int64_t>(1, std::min<int64_t>(want, int64_t(1) << 20));
+  if (idx32)
+    ew_generic_kernel<TI, TO, NI, NO, true, F>
+        <<<dim3(unsigned(blocks)), EW_THREADS, 0, s>>>(pin, pout, st, sh, n,
+                                                        f);
+  else
+    ew_generic_kernel<TI, TO, NI, NO, false, F>
+        <<<dim3(unsigned(blocks)), EW_THREADS, 0, s>>>(pin, pout, st, sh, n,
+                                                        f);
+  NT_LAUNCH_CHECK();
+}
+
+// Validates that every view has the same shape as the first one.
+inline void require_views_same_shape(const nt_view *const *views, int n,
+                                     const char *fname) {
+  for (int k = 1; k < n; ++k)
+    require_same_shape(views[0], views[k], fname);
+}
+
+} // namespace nt

@@ -1,0 +1,488 @@
+// Batched matmul C[b] = A[b] . B[b] (+ C_old[b]) on strided views.
+//
+// fp32 runs on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32).  The
+// reference (src/cpp/ops/matmul.cu) has a SIMT 128x128x16 kernel that only
+// accepts contiguous operands and sends every transposed operand -- hence
+// both backward products of MatmulOp (ops_binary.py:264-267) -- to a naive
+// one-thread-per-output kernel.  Here each operand is read in place in
+// whichever orientation it has:
+//
+//   layout K  : the reduction index k is the unit-stride one (A row-major,
+//               or B = W^T of a row-major W).  Stored in LDS as [mn][k].
+//   layout MN : the m (or n) index is unit-stride (A = X^T of a row-major
+//               X, or B row-major).  Stored in LDS as [k][mn].
+//   layout GEN: anything else (e.g. `[:, ::2]` views): scalar loads, stored
+//               as [mn][k].
+//
+// Workgroup tile 128x128, k-tile 32, 256 threads = 4 waves in a 2x2 grid,
+// each wave owns a 64x64 block = 2x2 MFMA 32x32 blocks (64 accumulator
+// registers per lane).  Global loads for k-tile t+1 are issued before the
+// MFMAs of tile t; LDS is double buffered so one barrier per k-tile
+// suffices.  Workgroups are numbered so that consecutive tiles of a group of
+// 8 tile-rows land on the same XCD (gfx950 dispatches workgroups round-robin
+// over its 8 XCDs, each with its own L2).
+//
+// MFMA k assignment: in MFMA step kk (0..15) of a k-tile, the lanes of wave
+// half h (lane / 32) supply k = h*16 + kk, for A and B alike, so each lane's
+// 16 fragments of a k-tile are contiguous in a [mn][k] LDS row.  The sum over
+// k is unchanged; only the fp32 accumulation order differs from the
+// reference's sequential loop (|diff| <= 1e-4 * (|A|.|B|) is the parity
+// bound).  Accumulate mode adds C_old after the full dot product: one
+// rounding, like the reference's `x._grad += grad`.
+//
+// Other dtypes (fp64, int32, int64) use a tiled SIMT kernel that accumulates
+// in k order exactly like the reference's CPU loop (matmul.cu:33-45).
+#include <algorithm>
+
+#include "nt_internal.h"
+
+namespace nt {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int MM_BM = 128, MM_BN = 128, MM_BK = 32, MM_THREADS = 256;
+constexpr int MM_KPAD = MM_BK + 4;  // [mn][k] row length (floats)
+constexpr int MM_MNPAD = MM_BM + 4; // [k][mn] row length (floats)
+constexpr int MM_REGION = (MM_BM * MM_KPAD > MM_BK * MM_MNPAD)
+                              ? MM_BM * MM_KPAD
+                              : MM_BK * MM_MNPAD; // floats per operand stage
+constexpr int MM_MAX_BATCH = NT_MAX_DIMS - 2;
+
+enum { LAY_K = 0, LAY_MN = 1, LAY_GEN = 2 };
+
+struct MMArgs {
+  const float *A;
+  const float *B;
+  float *C;
+  int64_t M, N, K;
+  int64_t sAm, sAk, sBk, sBn, sCm, sCn;
+  int nb;
+  int64_t bshape[MM_MAX_BATCH];
+  int64_t bsA[MM_MAX_BATCH], bsB[MM_MAX_BATCH], bsC[MM_MAX_BATCH];
+  int64_t tiles_m, tiles_n;
+  int accumulate;
+};
+
+// Operand tile loader: global -> registers -> LDS.  ROWS x MM_BK tile of
+// the operand in (mn, k) coordinates, where mn is m for A and n for B.
+// s_mn / s_k are the element strides of the mn and k indices.
+template <int LAY> struct TileLoad {
+  float4 r[4];
+  __device__ __forceinline__ void load(const float *p, int64_t mn0, int64_t k0,
+                                       int64_t MN, int64_t K, int64_t s_mn,
+                                       int64_t s_k, int t) {
+    if constexpr (LAY == LAY_K) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t mn = mn0 + (t >> 3) + 32 * i;
+        const int64_t k = k0 + (t & 7) * 4;
+        if (mn < MN && k < K)
+          r[i] = *reinterpret_cast<const float4 *>(p + mn * s_mn + k);
+        else
+          r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    } else if constexpr (LAY == LAY_MN) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t k = k0 + (t >> 5) + 8 * i;
+        const int64_t mn = mn0 + (t & 31) * 4;
+        if (mn < MN && k < K)
+          r[i] = *reinterpret_cast<const float4 *>(p + mn + k * s_k);
+        else
+          r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int flat = t + MM_THREADS * (4 * i + q); // 0..4095
+          const int64_t mn = mn0 + (flat >> 5);
+          const int64_t k = k0 + (flat & 31);
+          v[q] = (mn < MN && k < K) ? p[mn * s_mn + k * s_k] : 0.f;
+        }
+        r[i] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float *lds, int t) const {
+    if constexpr (LAY == LAY_K) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int mn = (t >> 3) + 32 * i, k = (t & 7) * 4;
+        *reinterpret_cast<float4 *>(lds + mn * MM_KPAD + k) = r[i];
+      }
+    } else if constexpr (LAY == LAY_MN) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = (t >> 5) + 8 * i, mn = (t & 31) * 4;
+        *reinterpret_cast<float4 *>(lds + k * MM_MNPAD + mn) = r[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int flat = t + MM_THREADS * (4 * i + q);
+          lds[(flat >> 5) * MM_KPAD + (flat & 31)] = v[q];
+        }
+      }
+    }
+  }
+};
+
+// Fragment read: element (mn, k) of the staged tile.
+template <int LAY>
+__device__ __forceinline__ float frag(const float *lds, int mn, int k) {
+  if constexpr (LAY == LAY_MN)
+    return lds[k * MM_MNPAD + mn];
+  else
+    return lds[mn * MM_KPAD + k];
+}
+
+template <int LA, int LB>
+__global__ __launch_bounds__(MM_THREADS, 2) void mm_f32_mfma_kernel(MMArgs g) {
+  __shared__ __align__(16) float lds[2][2][MM_REGION]; // [stage][A/B]
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int h = lane >> 5, li = lane & 31;
+
+  // ---- tile coordinates: XCD-contiguous numbering, then groups of 8
+  // tile-rows walked column by column.
+  const int64_t ntiles = g.tiles_m * g.tiles_n;
+  const int64_t per_batch = ntiles;
+  int64_t bid = blockIdx.x;
+  const int64_t nblk = gridDim.x;
+  if (nblk % 8 == 0)
+    bid = (bid % 8) * (nblk / 8) + bid / 8;
+  const int64_t batch = bid / per_batch;
+  const int64_t tile = bid - batch * per_batch;
+  constexpr int64_t GROUP = 8;
+  const int64_t group = tile / (GROUP * g.tiles_n);
+  const int64_t first_m = group * GROUP;
+  const int64_t gsize = (g.tiles_m - first_m) < GROUP ? (g.tiles_m - first_m)
+                                                       : GROUP;
+  const int64_t in_group = tile - group * GROUP * g.tiles_n;
+  const int64_t tm = first_m + in_group % gsize;
+  const int64_t tn = in_group / gsize;
+  const int64_t m0 = tm * MM_BM, n0 = tn * MM_BN;
+
+  // ---- batch offsets
+  const float *A = g.A;
+  const float *B = g.B;
+  float *C = g.C;
+  {
+    int64_t rem = batch;
+    for (int d = g.nb - 1; d >= 0; --d) {
+      const int64_t q = rem / g.bshape[d];
+      const int64_t c = rem - q * g.bshape[d];
+      rem = q;
+      A += c * g.bsA[d];
+      B += c * g.bsB[d];
+      C += c * g.bsC[d];
+    }
+  }
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc[i][j][r] = 0.f;
+
+  TileLoad<LA> la;
+  TileLoad<LB> lb;
+  const int64_t ktiles = (g.K + MM_BK - 1) / MM_BK;
+  la.load(A, m0, 0, g.M, g.K, g.sAm, g.sAk, t);
+  lb.load(B, n0, 0, g.N, g.K, g.sBn, g.sBk, t);
+  la.store(lds[0][0], t);
+  lb.store(lds[0][1], t);
+  __syncthreads();
+
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    const int cur = int(kt & 1);
+    if (kt + 1 < ktiles) {
+      la.load(A, m0, (kt + 1) * MM_BK, g.M, g.K, g.sAm, g.sAk, t);
+      lb.load(B, n0, (kt + 1) * MM_BK, g.N, g.K, g.sBn, g.sBk, t);
+    }
+    const float *As = lds[cur][0];
+    const float *Bs = lds[cur][1];
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      const int k = h * 16 + kk;
+      float a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = frag<LA>(As, wm * 64 + i * 32 + li, k);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        b[j] = frag<LB>(Bs, wn * 64 + j * 32 + li, k);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j],
+                                                           acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < ktiles) {
+      la.store(lds[cur ^ 1][0], t);
+      lb.store(lds[cur ^ 1][1], t);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds column li of each 32x32 block, rows
+  // 8*(r/4) + 4*h + (r%4).
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + wn * 64 + j * 32 + li;
+      if (col >= g.N)
+        continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row =
+            m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        if (row < g.M) {
+          float *dst = C + row * g.sCm + col * g.sCn;
+          const float v = acc[i][j][r];
+          *dst = g.accumulate ? (*dst + v) : v;
+        }
+      }
+    }
+}
+
+// ------------------------------------------------ SIMT (non-fp32) kernel
+
+template <class T> struct MMArgsT {
+  const T *A;
+  const T *B;
+  T *C;
+  int64_t M, N, K;
+  int64_t sAm, sAk, sBk, sBn, sCm, sCn;
+  int nb;
+  int64_t bshape[MM_MAX_BATCH];
+  int64_t bsA[MM_MAX_BATCH], bsB[MM_MAX_BATCH], bsC[MM_MAX_BATCH];
+  int accumulate;
+};
+
+template <class T>
+__global__ __launch_bounds__(256) void mm_simt_kernel(MMArgsT<T> g) {
+  constexpr int TS = 16;
+  __shared__ T As[TS][TS + 1];
+  __shared__ T Bs[TS][TS + 1];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t row = int64_t(blockIdx.y) * TS + ty;
+  const int64_t col = int64_t(blockIdx.x) * TS + tx;
+  const T *A = g.A;
+  const T *B = g.B;
+  T *C = g.C;
+  int64_t rem = blockIdx.z;
+  for (int d = g.nb - 1; d >= 0; --d) {
+    const int64_t q = rem / g.bshape[d];
+    const int64_t c = rem - q * g.bshape[d];
+    rem = q;
+    A += c * g.bsA[d];
+    B += c * g.bsB[d];
+    C += c * g.bsC[d];
+  }
+  T acc = T(0);
+  for (int64_t k0 = 0; k0 < g.K; k0 += TS) {
+    const int64_t ka = k0 + tx, kb = k0 + ty;
+    As[ty][tx] = (row < g.M && ka < g.K) ? A[row * g.sAm + ka * g.sAk] : T(0);
+    Bs[ty][tx] = (kb < g.K && col < g.N) ? B[kb * g.sBk + col * g.sBn] : T(0);
+    __syncthreads();
+    const int kmax = (g.K - k0) < TS ? int(g.K - k0) : TS;
+    for (int k = 0; k < kmax; ++k)
+      acc = acc + As[ty][k] * Bs[k][tx];
+    __syncthreads();
+  }
+  if (row < g.M && col < g.N) {
+    T *dst = C + row * g.sCm + col * g.sCn;
+    *dst = g.accumulate ? T(*dst + acc) : acc;
+  }
+}
+
+namespace {
+
+template <int LA, int LB> void launch_mfma(const MMArgs &a, int64_t blocks) {
+  mm_f32_mfma_kernel<LA, LB>
+      <<<dim3(unsigned(blocks)), MM_THREADS, 0, stream()>>>(a);
+}
+
+template <int LA> void launch_mfma_b(int lb, const MMArgs &a, int64_t blocks) {
+  switch (lb) {
+  case LAY_K:
+    return launch_mfma<LA, LAY_K>(a, blocks);
+  case LAY_MN:
+    return launch_mfma<LA, LAY_MN>(a, blocks);
+  default:
+    return launch_mfma<LA, LAY_GEN>(a, blocks);
+  }
+}
+
+bool aligned16(const void *p) {
+  return reinterpret_cast<uintptr_t>(p) % 16 == 0;
+}
+
+} // namespace
+} // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
+              int32_t accumulate) {
+  return guard([&] {
+    check_view(a, "matmul");
+    check_view(b, "matmul");
+    check_view(c, "matmul");
+    if (a->dtype != b->dtype || a->dtype != c->dtype)
+      fail(NT_ERR_RUNTIME, "matmul: dtype mismatch");
+    if (a->ndim != b->ndim || a->ndim != c->ndim)
+      fail(NT_ERR_VALUE, "matmul: x1 and x2 have different ndim.");
+    if (a->ndim < 2)
+      fail(NT_ERR_VALUE, "matmul: kernel should be called with >=2d tensors.");
+    const int nd = a->ndim, nb = nd - 2;
+    for (int d = 0; d < nb; ++d)
+      if (a->shape[d] != b->shape[d] || a->shape[d] != c->shape[d])
+        fail(NT_ERR_VALUE, "Invalid broacast shapes.");
+    const int64_t M = a->shape[nd - 2], K = a->shape[nd - 1];
+    const int64_t N = b->shape[nd - 1];
+    if (b->shape[nd - 2] != K)
+      fail(NT_ERR_VALUE, "Invalid matmul shape.");
+    if (c->shape[nd - 2] != M || c->shape[nd - 1] != N)
+      fail(NT_ERR_RUNTIME, "matmul: output shape mismatch");
+    if (a->dtype == NT_BOOL)
+      fail(NT_ERR_VALUE, "Invalid dtype.");
+    int64_t nbatch = 1;
+    for (int d = 0; d < nb; ++d)
+      nbatch *= a->shape[d];
+    if (M == 0 || N == 0 || nbatch == 0)
+      return;
+    if (K == 0) {
+      if (!accumulate) {
+        dispatch_arith(c->dtype, [&]<class T>() {
+          // C = 0 through the copy kernel from a broadcast zero.
+          T *zero = static_cast<T *>(device_alloc(sizeof(T)));
+          NT_HIP_CHECK(hipMemsetAsync(zero, 0, sizeof(T), stream()));
+          nt_view zv = *c;
+          zv.data = zero;
+          zv.offset = 0;
+          for (int d = 0; d < zv.ndim; ++d)
+            zv.strides[d] = 0;
+          const int rc = nt_copy(&zv, c);
+          device_free(zero);
+          if (rc != NT_OK)
+            fail(rc, nt_last_error());
+        });
+      }
+      return;
+    }
+    // Size-1 dims carry no stride information; normalise them to 0.
+    auto st = [](const nt_view *v, int d) {
+      return v->shape[d] == 1 ? int64_t(0) : v->strides[d];
+    };
+    const int64_t sAm = st(a, nd - 2), sAk = st(a, nd - 1);
+    const int64_t sBk = st(b, nd - 2), sBn = st(b, nd - 1);
+    const int64_t sCm = c->strides[nd - 2], sCn = c->strides[nd - 1];
+
+    if (a->dtype == NT_FLOAT32) {
+      MMArgs g{};
+      g.A = typed_ptr<const float>(a);
+      g.B = typed_ptr<const float>(b);
+      g.C = typed_ptr<float>(c);
+      g.M = M;
+      g.N = N;
+      g.K = K;
+      g.sAm = sAm;
+      g.sAk = sAk;
+      g.sBk = sBk;
+      g.sBn = sBn;
+      g.sCm = sCm;
+      g.sCn = sCn;
+      g.nb = nb;
+      bool batch_al = true;
+      for (int d = 0; d < nb; ++d) {
+        g.bshape[d] = a->shape[d];
+        g.bsA[d] = st(a, d);
+        g.bsB[d] = st(b, d);
+        g.bsC[d] = st(c, d);
+        if (g.bsA[d] % 4 != 0 || g.bsB[d] % 4 != 0)
+          batch_al = false;
+      }
+      g.accumulate = accumulate ? 1 : 0;
+      // Vector (16-byte) tile loads need the unit-stride extent and the other
+      // stride to be multiples of 4 and a 16-byte aligned base.
+      int la = LAY_GEN, lb = LAY_GEN;
+      if (batch_al && aligned16(g.A)) {
+        if (sAk == 1 && sAm % 4 == 0 && K % 4 == 0)
+          la = LAY_K;
+        else if (sAm == 1 && sAk % 4 == 0 && M % 4 == 0)
+          la = LAY_MN;
+      }
+      if (batch_al && aligned16(g.B)) {
+        if (sBn == 1 && sBk % 4 == 0 && N % 4 == 0)
+          lb = LAY_MN;
+        else if (sBk == 1 && sBn % 4 == 0 && K % 4 == 0)
+          lb = LAY_K;
+      }
+      g.tiles_m = (M + MM_BM - 1) / MM_BM;
+      g.tiles_n = (N + MM_BN - 1) / MM_BN;
+      const int64_t blocks = g.tiles_m * g.tiles_n * nbatch;
+      if (blocks >= (int64_t(1) << 31))
+        fail(NT_ERR_RUNTIME, "matmul: problem too large");
+      switch (la) {
+      case LAY_K:
+        launch_mfma_b<LAY_K>(lb, g, blocks);
+        break;
+      case LAY_MN:
+        launch_mfma_b<LAY_MN>(lb, g, blocks);
+        break;
+      default:
+        launch_mfma_b<LAY_GEN>(lb, g, blocks);
+      }
+      NT_LAUNCH_CHECK();
+      return;
+    }
+
+    dispatch_arith(a->dtype, [&]<class T>() {
+      MMArgsT<T> g{};
+      g.A = typed_ptr<const T>(a);
+      g.B = typed_ptr<const T>(b);
+      g.C = typed_ptr<T>(c);
+      g.M = M;
+      g.N = N;
+      g.K = K;
+      g.sAm = sAm;
+      g.sAk = sAk;
+      g.sBk = sBk;
+      g.sBn = sBn;
+      g.sCm = sCm;
+      g.sCn = sCn;
+      g.nb = nb;
+      for (int d = 0; d < nb; ++d) {
+        g.bshape[d] = a->shape[d];
+        g.bsA[d] = st(a, d);
+        g.bsB[d] = st(b, d);
+        g.bsC[d] = st(c, d);
+      }
+      g.accumulate = accumulate ? 1 : 0;
+      if (nbatch > 65535)
+        fail(NT_ERR_RUNTIME, "matmul: too many batches for the SIMT path");
+      dim3 grid{unsigned((N + 15) / 16), unsigned((M + 15) / 16),
+                unsigned(nbatch)};
+      mm_simt_kernel<T><<<grid, 256, 0, stream()>>>(g);
+      NT_LAUNCH_CHECK();
+    });
+  });
+}
+
+} // extern "C"

@@ -1,0 +1,751 @@
+// Axis reductions (sum / max / min / argmax / argmin) and their backward.
+//
+// Semantics follow src/cpp/ops/reduction_ops.cu:
+//  * the reduced axes form a "drop" view whose row-major order follows the
+//    caller's axis tuple; the reduced index j of an element is its position
+//    in that order (:187-217);
+//  * sum accumulates in the output dtype, each element cast first (:66-67);
+//  * max/min keep the first j on ties; the neutral elements are
+//    (numeric_limits::lowest / max, j = INT64_MAX) (:13-40), so a slice whose
+//    values are all below lowest() (i.e. -inf) reports lowest() and
+//    INT64_MAX, as the reference does.
+// The reference reduces each slice sequentially on the CPU and with a
+// multi-pass shared-memory tree over 16-byte (idx, value) partials on CUDA.
+//
+// Kernels here, by layout of the slice elements in memory:
+//  * row    -- each slice is one contiguous run (e.g. axis=-1, or a full
+//              reduction of a contiguous tensor): workgroups stream the run
+//              with 16-byte loads; a wave combines with cross-lane shuffles
+//              and the four waves through LDS.  Long runs are split into S
+//              segments whose partials a second kernel combines in order.
+//  * column -- the kept axis is the contiguous one (e.g. axis=0 of a
+//              row-major matrix): each lane owns 4 adjacent columns and walks
+//              rows, so every wave load is 1 KB contiguous; rows are split
+//              across S workgroups and a second kernel combines partials.
+//  * generic-- anything else: one workgroup per (slice, segment), elements
+//              located by multiply-high unravel of j over the drop view.
+// Max/min carry (value, first j, count of elements equal to the extremum);
+// the count is what the backward needs (see nt_reduce_bwd).
+//
+// Sums are combined in a different order than the reference's sequential
+// loop, so they agree to within rounding (|diff| <= 1e-5 * sum|x| is the
+// parity bound); max/min/arg results are exact.
+#include <limits>
+
+#include "ew_engine.h"
+
+namespace nt {
+
+constexpr int RED_THREADS = 256;
+constexpr int RED_WAVES = RED_THREADS / 64;
+
+// ------------------------------------------------------------ accumulators
+
+template <class O> struct SumAcc {
+  O s;
+  __device__ __forceinline__ void init() { s = O(0); }
+  __device__ __forceinline__ void add(O x, int64_t) { s = s + x; }
+  // `o` covers elements after this one's.
+  __device__ __forceinline__ void merge(const SumAcc &o) { s = s + o.s; }
+  __device__ __forceinline__ void shfl_merge(int off) {
+    SumAcc o;
+    o.s = __shfl_xor(s, off, 64);
+    merge(o);
+  }
+};
+
+template <class O, bool IS_MAX> struct SelAcc {
+  O v;
+  int64_t j;
+  int32_t c;
+  __device__ __forceinline__ void init() {
+    v = IS_MAX ? std::numeric_limits<O>::lowest()
+               : std::numeric_limits<O>::max();
+    j = std::numeric_limits<int64_t>::max();
+    c = 0;
+  }
+  __device__ __forceinline__ static bool better(O a, O b) {
+    if constexpr (IS_MAX)
+      return a > b;
+    else
+      return a < b;
+  }
+  __device__ __forceinline__ void add(O x, int64_t jj) {
+    if (better(x, v)) {
+      v = x;
+      j = jj;
+      c = 1;
+    } else if (x == v) {
+      j = jj < j ? jj : j;
+      c += 1;
+    }
+  }
+  __device__ __forceinline__ void merge(const SelAcc &o) {
+    if (better(o.v, v)) {
+      v = o.v;
+      j = o.j;
+      c = o.c;
+    } else if (o.v == v) {
+      j = o.j < j ? o.j : j;
+      c += o.c;
+    }
+  }
+  __device__ __forceinline__ void shfl_merge(int off) {
+    SelAcc o;
+    if constexpr (std::is_same_v<O, bool>)
+      o.v = bool(__shfl_xor(int(v), off, 64));
+    else
+      o.v = __shfl_xor(v, off, 64);
+    o.j = __shfl_xor(j, off, 64);
+    o.c = __shfl_xor(c, off, 64);
+    merge(o);
+  }
+};
+
+// Writes the final accumulator of slice k.
+// MODE 0: sum value; 1: extremum value (+ optional idx/count); 2: index.
+template <int MODE> struct RedOut {
+  void *val;
+  int64_t *idx;
+  int32_t *cnt;
+  template <class O, class Acc>
+  __device__ __forceinline__ void write(int64_t k, const Acc &a) const {
+    if constexpr (MODE == 0) {
+      static_cast<O *>(val)[k] = a.s;
+    } else if constexpr (MODE == 1) {
+      static_cast<O *>(val)[k] = a.v;
+      if (idx)
+        idx[k] = a.j;
+      if (cnt)
+        cnt[k] = a.c;
+    } else {
+      static_cast<int64_t *>(val)[k] = a.j;
+    }
+  }
+};
+
+template <class Acc> __device__ __forceinline__ void wave_reduce(Acc &a) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1)
+    a.shfl_merge(off);
+}
+
+// Reduces the 4 waves' accumulators (wave order) into wave 0's lane 0 value,
+// returned to every thread of wave 0.
+template <class Acc>
+__device__ __forceinline__ Acc block_reduce(Acc a, Acc *lds) {
+  wave_reduce(a);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0)
+    lds[w] = a;
+  __syncthreads();
+  Acc r = lds[0];
+#pragma unroll
+  for (int i = 1; i < RED_WAVES; ++i)
+    r.merge(lds[i]);
+  return r;
+}
+
+struct KeepDesc {
+  int ndim;
+  int64_t shape[NT_MAX_DIMS];
+  int64_t strides[NT_MAX_DIMS];
+  __device__ __forceinline__ int64_t offset_of(int64_t k) const {
+    int64_t off = 0;
+    for (int d = ndim - 1; d >= 0; --d) {
+      const int64_t q = k / shape[d];
+      off += (k - q * shape[d]) * strides[d];
+      k = q;
+    }
+    return off;
+  }
+};
+
+struct DropDesc {
+  int ndim;
+  int64_t shape[NT_MAX_DIMS];
+  int64_t strides[NT_MAX_DIMS];
+  FastDivU32 fd[NT_MAX_DIMS];
+};
+
+// ---------------------------------------------------------------- kernels
+
+// Slices are contiguous runs of length D starting at x + keep.offset_of(k).
+// Block b handles slice k = b / S, segment s = b % S: j in [s*seg, ..).
+template <class T, class O, class Acc, int VEC, int MODE>
+__global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
+    const T *__restrict__ x, KeepDesc keep, int64_t D, int64_t seg, int S,
+    Acc *partial, RedOut<MODE> out) {
+  __shared__ Acc lds[RED_WAVES];
+  const int64_t k = int64_t(blockIdx.x) / S;
+  const int s = int(int64_t(blockIdx.x) - k * S);
+  const T *row = x + keep.offset_of(k);
+  const int64_t j0 = int64_t(s) * seg;
+  const int64_t j1 = j0 + seg < D ? j0 + seg : D;
+  Acc a;
+  a.init();
+  using V = VecT<T, VEC>;
+  for (int64_t j = j0 + int64_t(threadIdx.x) * VEC; j < j1;
+       j += int64_t(RED_THREADS) * VEC) {
+    if (VEC > 1 && j + VEC <= j1) {
+      const V v = *reinterpret_cast<const V *>(row + j);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        a.add(static_cast<O>(v.v[i]), j + i);
+    } else {
+      for (int i = 0; i < VEC && j + i < j1; ++i)
+        a.add(static_cast<O>(row[j + i]), j + i);
+    }
+  }
+  Acc r = block_reduce(a, lds);
+  if (threadIdx.x == 0) {
+    if (S == 1)
+      out.template write<O>(k, r);
+    else
+      partial[k * S + s] = r;
+  }
+}
+
+// x is [D, K] with K contiguous (stride 1) and row stride sd.  Block
+// (bx, s): columns [bx*64*VEC, +64*VEC), rows [s*seg, ..).  Lane l owns VEC
+// adjacent columns; wave w walks rows w, w+4, ...
+template <class T, class O, class Acc, int VEC, int MODE>
+__global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
+    const T *__restrict__ x, int64_t K, int64_t D, int64_t sd, int64_t seg,
+    int S, Acc *partial, RedOut<MODE> out) {
+  __shared__ Acc lds[RED_WAVES][64 * VEC];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int s = blockIdx.y;
+  const int64_t k0 = int64_t(blockIdx.x) * 64 * VEC + int64_t(lane) * VEC;
+  const int64_t j0 = int64_t(s) * seg;
+  const int64_t j1 = j0 + seg < D ? j0 + seg : D;
+  Acc a[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+    a[i].init();
+  using V = VecT<T, VEC>;
+  if (k0 + VEC <= K) {
+    for (int64_t j = j0 + w; j < j1; j += RED_WAVES) {
+      const V v = *reinterpret_cast<const V *>(x + j * sd + k0);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        a[i].add(static_cast<O>(v.v[i]), j);
+    }
+  } else {
+    for (int64_t j = j0 + w; j < j1; j += RED_WAVES)
+      for (int i = 0; i < VEC; ++i)
+        if (k0 + i < K)
+          a[i].add(static_cast<O>(x[j * sd + k0 + i]), j);
+  }
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+    lds[w][lane * VEC + i] = a[i];
+  __syncthreads();
+  if (w == 0) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      Acc r = lds[0][lane * VEC + i];
+#pragma unroll
+      for (int ww = 1; ww < RED_WAVES; ++ww)
+        r.merge(lds[ww][lane * VEC + i]);
+      const int64_t k = k0 + i;
+      if (k < K) {
+        if (S == 1)
+          out.template write<O>(k, r);
+        else
+          partial[k * S + s] = r;
+      }
+    }
+  }
+}
+
+template <class T, class O, class Acc, int MODE>
+__global__ __launch_bounds__(RED_THREADS) void reduce_generic_kernel(
+    const T *__restrict__ x, KeepDesc keep, DropDesc drop, int64_t D,
+    int64_t seg, int S, bool idx32, Acc *partial, RedOut<MODE> out) {
+  __shared__ Acc lds[RED_WAVES];
+  const int64_t k = int64_t(blockIdx.x) / S;
+  const int s = int(int64_t(blockIdx.x) - k * S);
+  const T *base = x + keep.offset_of(k);
+  const int64_t j0 = int64_t(s) * seg;
+  const int64_t j1 = j0 + seg < D ? j0 + seg : D;
+  Acc a;
+  a.init();
+  for (int64_t j = j0 + threadIdx.x; j < j1; j += RED_THREADS) {
+    int64_t off = 0;
+    if (idx32) {
+      uint32_t rem = uint32_t(j);
+      for (int d = drop.ndim - 1; d >= 0; --d) {
+        const uint32_t q = drop.fd[d].div(rem);
+        off += int64_t(rem - q * uint32_t(drop.shape[d])) * drop.strides[d];
+        rem = q;
+      }
+    } else {
+      int64_t rem = j;
+      for (int d = drop.ndim - 1; d >= 0; --d) {
+        const int64_t q = rem / drop.shape[d];
+        off += (rem - q * drop.shape[d]) * drop.strides[d];
+        rem = q;
+      }
+    }
+    a.add(static_cast<O>(base[off]), j);
+  }
+  Acc r = block_reduce(a, lds);
+  if (threadIdx.x == 0) {
+    if (S == 1)
+      out.template write<O>(k, r);
+    else
+      partial[k * S + s] = r;
+  }
+}
+
+// Combines the S partials of slice k (one wave per slice), in segment order
+// per lane, then across lanes.
+template <class O, class Acc, int MODE>
+__global__ __launch_bounds__(64) void reduce_combine_kernel(
+    const Acc *__restrict__ partial, int S, RedOut<MODE> out) {
+  const int64_t k = blockIdx.x;
+  Acc a;
+  a.init();
+  for (int s = threadIdx.x; s < S; s += 64)
+    a.merge(partial[k * S + s]);
+  wave_reduce(a);
+  if (threadIdx.x == 0)
+    out.template write<O>(k, a);
+}
+
+// ------------------------------------------------------------------- plan
+
+struct RedPlan {
+  int64_t K = 1, D = 1;
+  nt_view keep{}, drop{}; // coalesced, strides in elements; keep has offset
+};
+
+// Merges adjacent dims (in the order given) of a single view.
+void coalesce_single(nt_view &v) {
+  int out = 0;
+  for (int d = 0; d < v.ndim; ++d) {
+    if (v.shape[d] == 1)
+      continue;
+    if (out > 0 && v.strides[out - 1] == v.strides[d] * v.shape[d]) {
+      v.shape[out - 1] *= v.shape[d];
+      v.strides[out - 1] = v.strides[d];
+      continue;
+    }
+    v.shape[out] = v.shape[d];
+    v.strides[out] = v.strides[d];
+    ++out;
+  }
+  v.ndim = out;
+}
+
+RedPlan make_plan(const nt_view *x, const int64_t *axes, int naxes) {
+  RedPlan p;
+  bool is_drop[NT_MAX_DIMS] = {};
+  for (int i = 0; i < naxes; ++i) {
+    const int64_t ax = axes[i];
+    if (ax < 0 || ax >= x->ndim)
+      fail(NT_ERR_INDEX, "reduction: axis out of range");
+    if (is_drop[ax])
+      fail(NT_ERR_VALUE, "reduction: redundant axes");
+    is_drop[ax] = true;
+  }
+  p.keep.ndim = 0;
+  for (int d = 0; d < x->ndim; ++d)
+    if (!is_drop[d]) {
+      p.keep.shape[p.keep.ndim] = x->shape[d];
+      p.keep.strides[p.keep.ndim] = x->strides[d];
+      p.keep.ndim++;
+      p.K *= x->shape[d];
+    }
+  p.drop.ndim = naxes;
+  for (int i = 0; i < naxes; ++i) {
+    p.drop.shape[i] = x->shape[axes[i]];
+    p.drop.strides[i] = x->strides[axes[i]];
+    p.D *= x->shape[axes[i]];
+  }
+  coalesce_single(p.keep);
+  coalesce_single(p.drop);
+  return p;
+}
+
+KeepDesc to_keep_desc(const nt_view &v) {
+  KeepDesc k{};
+  k.ndim = v.ndim;
+  for (int d = 0; d < v.ndim; ++d) {
+    k.shape[d] = v.shape[d];
+    k.strides[d] = v.strides[d];
+  }
+  return k;
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+template <class T, class O, class Acc, int MODE>
+void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
+  if (p.K == 0)
+    return;
+  const T *xp = typed_ptr<const T>(x);
+  hipStream_t st = stream();
+  const int64_t target_blocks = int64_t(device_cu_count()) * 8;
+  constexpr int VEC = std::is_same_v<T, O> ? ew_vec<T>() : 1;
+  constexpr bool FAST = std::is_same_v<T, O> &&
+                        (std::is_same_v<T, float> || std::is_same_v<T, double>);
+
+  auto finish = [&](Acc *partial, int S) {
+    if (S > 1) {
+      reduce_combine_kernel<O, Acc, MODE>
+          <<<dim3(unsigned(p.K)), 64, 0, st>>>(partial, S, out);
+      NT_LAUNCH_CHECK();
+    }
+    if (partial)
+      device_free(partial);
+  };
+
+  const bool drop_contig =
+      p.drop.ndim == 0 || (p.drop.ndim == 1 && p.drop.strides[0] == 1);
+  const bool col_layout = p.drop.ndim == 1 && p.keep.ndim == 1 &&
+                          p.keep.strides[0] == 1 && p.drop.strides[0] != 1;
+
+  if (FAST && drop_contig) {
+    // Vector loads need every slice start and segment start VEC-aligned.
+    bool aligned = reinterpret_cast<uintptr_t>(xp) % (sizeof(T) * VEC) == 0;
+    for (int d = 0; d < p.keep.ndim; ++d)
+      if (p.keep.strides[d] % VEC != 0)
+        aligned = false;
+    int64_t S = 1;
+    if (p.K < target_blocks)
+      S = std::min<int64_t>(ceil_div(target_blocks, p.K),
+                            std::max<int64_t>(1, p.D / (RED_THREADS * 16)));
+    S = std::max<int64_t>(1, std::min<int64_t>(S, 1 << 16));
+    int64_t seg = ceil_div(p.D, S);
+    seg = ceil_div(seg, VEC) * VEC;
+    S = ceil_div(p.D, seg);
+    Acc *partial =
+        S > 1 ? static_cast<Acc *>(device_alloc(sizeof(Acc) * p.K * S))
+              : nullptr;
+    const KeepDesc kd = to_keep_desc(p.keep);
+    const int64_t blocks = p.K * S;
+    if (blocks >= (int64_t(1) << 31))
+      fail(NT_ERR_RUNTIME, "reduction too large");
+    if (aligned)
+      reduce_row_kernel<T, O, Acc, VEC, MODE>
+          <<<dim3(unsigned(blocks)), RED_THREADS, 0, st>>>(
+              xp, kd, p.D, seg, int(S), partial, out);
+    else
+      reduce_row_kernel<T, O, Acc, 1, MODE>
+          <<<dim3(unsigned(blocks)), RED_THREADS, 0, st>>>(
+              xp, kd, p.D, seg, int(S), partial, out);
+    NT_LAUNCH_CHECK();
+    finish(partial, int(S));
+    return;
+  }
+
+  if (FAST && col_layout) {
+    const int64_t K = p.keep.shape[0], D = p.drop.shape[0];
+    const int64_t sd = p.drop.strides[0];
+    const bool aligned =
+        reinterpret_cast<uintptr_t>(xp) % (sizeof(T) * VEC) == 0 &&
+        sd % VEC == 0;
+    const int vec = aligned ? VEC : 1;
+    const int64_t bx = ceil_div(K, 64 * vec);
+    int64_t S = std::max<int64_t>(1, ceil_div(target_blocks, bx));
+    S = std::min<int64_t>(S, std::max<int64_t>(1, D / (RED_WAVES * 8)));
+    S = std::min<int64_t>(S, 65535);
+    const int64_t seg = ceil_div(D, S);
+    S = ceil_div(D, seg);
+    Acc *partial =
+        S > 1 ? static_cast<Acc *>(device_alloc(sizeof(Acc) * K * S))
+              : nullptr;
+    if (bx >= (int64_t(1) << 31))
+      fail(NT_ERR_RUNTIME, "reduction too large");
+    const dim3 grid{unsigned(bx), unsigned(S), 1u};
+    if (aligned)
+      reduce_col_kernel<T, O, Acc, VEC, MODE><<<grid, RED_THREADS, 0, st>>>(
+          xp, K, D, sd, seg, int(S), partial, out);
+    else
+      reduce_col_kernel<T, O, Acc, 1, MODE><<<grid, RED_THREADS, 0, st>>>(
+          xp, K, D, sd, seg, int(S), partial, out);
+    NT_LAUNCH_CHECK();
+    finish(partial, int(S));
+    return;
+  }
+
+  // generic
+  DropDesc dd{};
+  dd.ndim = p.drop.ndim;
+  const bool idx32 = p.D < (int64_t(1) << 32);
+  for (int d = 0; d < p.drop.ndim; ++d) {
+    dd.shape[d] = p.drop.shape[d];
+    dd.strides[d] = p.drop.strides[d];
+    if (idx32)
+      dd.fd[d] = FastDivU32(uint32_t(p.drop.shape[d]));
+  }
+  int64_t S = 1;
+  if (p.K < target_blocks)
+    S = std::min<int64_t>(ceil_div(target_blocks, p.K),
+                          std::max<int64_t>(1, p.D / (RED_THREADS * 8)));
+  S = std::max<int64_t>(1, std::min<int64_t>(S, 1 << 16));
+  const int64_t seg = ceil_div(p.D, S);
+  S = ceil_div(p.D, seg);
+  Acc *partial = S > 1
+                     ? static_cast<Acc *>(device_alloc(sizeof(Acc) * p.K * S))
+                     : nullptr;
+  const int64_t blocks = p.K * S;
+  if (blocks >= (int64_t(1) << 31))
+    fail(NT_ERR_RUNTIME, "reduction too large");
+  reduce_generic_kernel<T, O, Acc, MODE>
+      <<<dim3(unsigned(blocks)), RED_THREADS, 0, st>>>(
+          xp, to_keep_desc(p.keep), dd, p.D, seg, int(S), idx32, partial, out);
+  NT_LAUNCH_CHECK();
+  finish(partial, int(S));
+}
+
+// -------------------------------------------------------------- backward
+
+// Max/min backward: gx[i] = g[k] * ((j == idx[k] && cnt[k] == 1) ? 1 : 0),
+// where (k, j) are the kept / reduced coordinates of logical element i.
+struct SelBwdDesc {
+  int ndim;
+  int64_t shape[NT_MAX_DIMS];
+  FastDivU32 fd[NT_MAX_DIMS];
+  int64_t gx_strides[NT_MAX_DIMS];
+  int64_t kmul[NT_MAX_DIMS]; // contribution of each coord to k
+  int64_t jmul[NT_MAX_DIMS]; // contribution of each coord to j
+};
+
+template <class T, bool ACC, bool IDX32>
+__global__ __launch_bounds__(256) void sel_bwd_kernel(
+    const T *__restrict__ g, const int64_t *__restrict__ idx,
+    const int32_t *__restrict__ cnt, T *gx, SelBwdDesc dsc, int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += stride) {
+    int64_t off = 0, k = 0, j = 0;
+    if constexpr (IDX32) {
+      uint32_t rem = uint32_t(i);
+#pragma unroll
+      for (int d = NT_MAX_DIMS - 1; d >= 0; --d)
+        if (d < dsc.ndim) {
+          const uint32_t q = dsc.fd[d].div(rem);
+          const int64_t c = int64_t(rem - q * uint32_t(dsc.shape[d]));
+          rem = q;
+          off += c * dsc.gx_strides[d];
+          k += c * dsc.kmul[d];
+          j += c * dsc.jmul[d];
+        }
+    } else {
+      int64_t rem = i;
+#pragma unroll
+      for (int d = NT_MAX_DIMS - 1; d >= 0; --d)
+        if (d < dsc.ndim) {
+          const int64_t q = rem / dsc.shape[d];
+          const int64_t c = rem - q * dsc.shape[d];
+          rem = q;
+          off += c * dsc.gx_strides[d];
+          k += c * dsc.kmul[d];
+          j += c * dsc.jmul[d];
+        }
+    }
+    const bool sel = (j == idx[k]) && (cnt[k] == 1);
+    const T t = g[k] * (sel ? T(1) : T(0));
+    if constexpr (ACC)
+      gx[off] = gx[off] + t;
+    else
+      gx[off] = t;
+  }
+}
+
+template <class T, bool ACC> struct BcastBwd {
+  T scale;
+  bool divide;
+  static constexpr int NI = ACC ? 2 : 1;
+  __device__ __forceinline__ void operator()(const T (&x)[NI],
+                                             T (&y)[1]) const {
+    const T t = divide ? x[0] / scale : x[0];
+    if constexpr (ACC)
+      y[0] = x[1] + t;
+    else
+      y[0] = t;
+  }
+};
+
+} // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_reduce(int32_t op, const nt_view *x, const int64_t *axes, int32_t naxes,
+              const nt_view *out, const nt_view *idx, const nt_view *count) {
+  return guard([&] {
+    check_view(x, "reduction");
+    check_view(out, "reduction");
+    if (naxes < 0 || naxes > x->ndim)
+      fail(NT_ERR_INDEX, "reduction: bad axis count");
+    if (naxes > 0 && !axes)
+      fail(NT_ERR_RUNTIME, "reduction: null axes");
+    RedPlan p = make_plan(x, axes, naxes);
+    if (numel(out) != p.K)
+      fail(NT_ERR_RUNTIME, "reduction: output size mismatch");
+    if (!is_contiguous(out))
+      fail(NT_ERR_RUNTIME, "reduction: output must be contiguous");
+    if (numel(x) == 0)
+      fail(NT_ERR_RUNTIME, "reduction: empty input");
+    if (op == NT_SUM) {
+      RedOut<0> ro{nullptr, nullptr, nullptr};
+      ro.val = static_cast<char *>(out->data) +
+               out->offset * int64_t(dtype_size(out->dtype));
+      dispatch_all(x->dtype, [&]<class T>() {
+        dispatch_arith(out->dtype, [&]<class O>() {
+          run_reduce<T, O, SumAcc<O>, 0>(x, p, ro);
+        });
+      });
+      return;
+    }
+    const bool is_max = (op == NT_MAX || op == NT_ARGMAX);
+    if (op == NT_MAX || op == NT_MIN) {
+      if (out->dtype != x->dtype)
+        fail(NT_ERR_RUNTIME, "reduction: max/min output dtype mismatch");
+      RedOut<1> ro{nullptr, nullptr, nullptr};
+      ro.val = static_cast<char *>(out->data) +
+               out->offset * int64_t(dtype_size(out->dtype));
+      if (idx) {
+        check_view(idx, "reduction");
+        if (idx->dtype != NT_INT64 || numel(idx) != p.K || !is_contiguous(idx))
+          fail(NT_ERR_RUNTIME, "reduction: idx must be contiguous int64");
+        ro.idx = typed_ptr<int64_t>(idx);
+      }
+      if (count) {
+        check_view(count, "reduction");
+        if (count->dtype != NT_INT32 || numel(count) != p.K ||
+            !is_contiguous(count))
+          fail(NT_ERR_RUNTIME, "reduction: count must be contiguous int32");
+        ro.cnt = typed_ptr<int32_t>(count);
+      }
+      dispatch_all(x->dtype, [&]<class T>() {
+        if (is_max)
+          run_reduce<T, T, SelAcc<T, true>, 1>(x, p, ro);
+        else
+          run_reduce<T, T, SelAcc<T, false>, 1>(x, p, ro);
+      });
+      return;
+    }
+    if (op == NT_ARGMAX || op == NT_ARGMIN) {
+      if (out->dtype != NT_INT64)
+        fail(NT_ERR_RUNTIME, "reduction: argmax/argmin output must be int64");
+      RedOut<2> ro{typed_ptr<int64_t>(out), nullptr, nullptr};
+      dispatch_all(x->dtype, [&]<class T>() {
+        if (is_max)
+          run_reduce<T, T, SelAcc<T, true>, 2>(x, p, ro);
+        else
+          run_reduce<T, T, SelAcc<T, false>, 2>(x, p, ro);
+      });
+      return;
+    }
+    fail(NT_ERR_VALUE, "reduction: unknown op");
+  });
+}
+
+int nt_reduce_bwd(int32_t op, const nt_view *g, double scale, const nt_view *idx,
+                  const nt_view *count, const int64_t *axes, int32_t naxes,
+                  const nt_view *gx, int32_t accumulate) {
+  return guard([&] {
+    check_view(g, "reduction_bwd");
+    check_view(gx, "reduction_bwd");
+    require_same_dtype(g, gx, "reduction_bwd");
+    if (naxes < 0 || naxes > gx->ndim || (naxes > 0 && !axes))
+      fail(NT_ERR_INDEX, "reduction_bwd: bad axes");
+    bool is_drop[NT_MAX_DIMS] = {};
+    for (int i = 0; i < naxes; ++i) {
+      if (axes[i] < 0 || axes[i] >= gx->ndim || is_drop[axes[i]])
+        fail(NT_ERR_INDEX, "reduction_bwd: bad axes");
+      is_drop[axes[i]] = true;
+    }
+    // Row-major multipliers of the kept coordinates (g is contiguous over
+    // the kept axes) and of the reduced coordinates in axis-tuple order.
+    int64_t kmul[NT_MAX_DIMS] = {}, jmul[NT_MAX_DIMS] = {};
+    int64_t K = 1, D = 1;
+    for (int d = gx->ndim - 1; d >= 0; --d)
+      if (!is_drop[d]) {
+        kmul[d] = K;
+        K *= gx->shape[d];
+      }
+    for (int i = naxes - 1; i >= 0; --i) {
+      jmul[axes[i]] = D;
+      D *= gx->shape[axes[i]];
+    }
+    if (numel(g) != K || !is_contiguous(g))
+      fail(NT_ERR_RUNTIME, "reduction_bwd: g must be contiguous over kept axes");
+    const int64_t n = numel(gx);
+    if (n == 0)
+      return;
+    const bool acc = accumulate != 0;
+    if (op == NT_SUM || op == NT_MEAN) {
+      nt_view gb = *gx;
+      gb.data = g->data;
+      gb.offset = g->offset;
+      for (int d = 0; d < gx->ndim; ++d)
+        gb.strides[d] = is_drop[d] ? 0 : kmul[d];
+      dispatch_float(g->dtype, [&]<class T>() {
+        const nt_view *outs[1] = {gx};
+        if (acc) {
+          const nt_view *ins[2] = {&gb, gx};
+          launch_elementwise<T, T, 2, 1>(
+              ins, outs, BcastBwd<T, true>{T(scale), op == NT_MEAN});
+        } else {
+          const nt_view *ins[1] = {&gb};
+          launch_elementwise<T, T, 1, 1>(
+              ins, outs, BcastBwd<T, false>{T(scale), op == NT_MEAN});
+        }
+      });
+      return;
+    }
+    if (op != NT_MAX && op != NT_MIN)
+      fail(NT_ERR_VALUE, "reduction_bwd: unknown op");
+    check_view(idx, "reduction_bwd");
+    check_view(count, "reduction_bwd");
+    if (idx->dtype != NT_INT64 || count->dtype != NT_INT32 ||
+        numel(idx) != K || numel(count) != K || !is_contiguous(idx) ||
+        !is_contiguous(count))
+      fail(NT_ERR_RUNTIME, "reduction_bwd: bad idx/count");
+    SelBwdDesc dsc{};
+    dsc.ndim = gx->ndim;
+    const bool idx32 = n < (int64_t(1) << 32);
+    for (int d = 0; d < gx->ndim; ++d) {
+      dsc.shape[d] = gx->shape[d];
+      if (idx32)
+        dsc.fd[d] = FastDivU32(uint32_t(gx->shape[d]));
+      dsc.gx_strides[d] = gx->strides[d];
+      dsc.kmul[d] = kmul[d];
+      dsc.jmul[d] = jmul[d];
+    }
+    const int64_t blocks =
+        std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256 * 4), 1 << 20));
+    dispatch_float(g->dtype, [&]<class T>() {
+      const T *gp = typed_ptr<const T>(g);
+      const int64_t *ip = typed_ptr<const int64_t>(idx);
+      const int32_t *cp = typed_ptr<const int32_t>(count);
+      T *op_ = typed_ptr<T>(gx);
+      hipStream_t st = stream();
+      if (acc) {
+        if (idx32)
+          sel_bwd_kernel<T, true, true>
+              <<<dim3(unsigned(blocks)), 256, 0, st>>>(gp, ip, cp, op_, dsc, n);
+        else
+          sel_bwd_kernel<T, true, false>
+              <<<dim3(unsigned(blocks)), 256, 0, st>>>(gp, ip, cp, op_, dsc, n);
+      } else {
+        if (idx32)
+          sel_bwd_kernel<T, false, true>
+              <<<dim3(unsigned(blocks)), 256, 0, st>>>(gp, ip, cp, op_, dsc, n);
+        else
+          sel_bwd_kernel<T, false, false>
+              <<<dim3(unsigned(blocks)), 256, 0, st>>>(gp, ip, cp, op_, dsc, n);
+      }
+      NT_LAUNCH_CHECK();
+    });
+  });
+}
+
+} // extern "C"

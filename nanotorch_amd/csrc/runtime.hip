@@ -1,0 +1,413 @@
+// Device runtime of libnt: initialisation, the library stream, the caching
+// allocator, host<->device copies, fills, timing events and the host RNG.
+//
+// Reference counterparts: src/cpp/cuda.{h,cpp} (availability, sync, error
+// checks), src/cpp/allocator.{h,cpp} (caching allocator), src/cpp/storage.cpp
+// (allocate/to/clone), src/cpp/factory.cu (fills) and src/cpp/random.h (RNG).
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <random>
+
+#include "nt_internal.h"
+
+namespace nt {
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Runtime {
+  bool initialised = false;
+  bool available = false;
+  int cu_count = 0;
+  hipStream_t stream = nullptr;
+};
+
+Runtime &rt() {
+  static Runtime r;
+  return r;
+}
+
+// ---------------------------------------------------------------- allocator
+//
+// Stream-ordered caching allocator.  Every kernel and copy of the library runs
+// on one stream, so a block freed by the host can be handed to the next
+// request immediately: any later use is queued after the last use of the
+// previous owner.  Requests are rounded up to 512 B (small) or 2 MiB (large)
+// so that the free lists see a handful of distinct sizes per workload.  On
+// an out-of-memory error the cache is returned to HIP and the request
+// retried once.  The reference's allocator buckets by 256 B and never frees
+// (src/cpp/allocator.cpp:16-36).
+struct CachingAllocator {
+  std::multimap<size_t, void *> free_blocks; // size -> ptr
+  std::map<void *, size_t> live;             // ptr -> size
+  size_t bytes_in_use = 0;
+  size_t bytes_cached = 0;
+
+  static size_t round_size(size_t n) {
+    if (n == 0)
+      n = 1;
+    const size_t small = 512, large = size_t(2) << 20;
+    if (n < large)
+      return (n + small - 1) / small * small;
+    return (n + large - 1) / large * large;
+  }
+
+  void *alloc(size_t nbytes) {
+    size_t sz = round_size(nbytes);
+    // Best fit among cached blocks no more than 25% larger than asked.
+    auto it = free_blocks.lower_bound(sz);
+    if (it != free_blocks.end() && it->first <= sz + sz / 4) {
+      void *p = it->second;
+      size_t bsz = it->first;
+      free_blocks.erase(it);
+      bytes_cached -= bsz;
+      live[p] = bsz;
+      bytes_in_use += bsz;
+      return p;
+    }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, sz);
+    if (e == hipErrorOutOfMemory) {
+      (void)hipGetLastError();
+      release_cache();
+      e = hipMalloc(&p, sz);
+    }
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      fail(NT_ERR_OOM, "device allocation of " + std::to_string(sz) +
+                           " bytes failed: " + hipGetErrorString(e));
+    }
+    live[p] = sz;
+    bytes_in_use += sz;
+    return p;
+  }
+
+  void free(void *p) {
+    auto it = live.find(p);
+    if (it == live.end())
+      fail(NT_ERR_RUNTIME, "nt_free: pointer not allocated by nt_malloc");
+    free_blocks.emplace(it->second, p);
+    bytes_cached += it->second;
+    bytes_in_use -= it->second;
+    live.erase(it);
+  }
+
+  void release_cache() {
+    if (free_blocks.empty())
+      return;
+    // Blocks may still be read by queued work of their previous owner.
+    NT_HIP_CHECK(hipStreamSynchronize(rt().stream));
+    for (auto &kv : free_blocks)
+      NT_HIP_CHECK(hipFree(kv.second));
+    free_blocks.clear();
+    bytes_cached = 0;
+  }
+};
+
+CachingAllocator &allocator() {
+  static CachingAllocator a;
+  return a;
+}
+
+std::mt19937_64 &host_rng() {
+  static std::mt19937_64 rng{std::random_device{}()};
+  return rng;
+}
+
+__global__ void fill_kernel_bytes(uint8_t *p, int64_t nbytes_pattern_units,
+                                  uint64_t pattern, int unit) {
+  // Generic fill for element sizes 1, 4 and 8 bytes: unit = element size.
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (; i < nbytes_pattern_units; i += stride) {
+    if (unit == 1)
+      p[i] = uint8_t(pattern);
+    else if (unit == 4)
+      reinterpret_cast<uint32_t *>(p)[i] = uint32_t(pattern);
+    else
+      reinterpret_cast<uint64_t *>(p)[i] = pattern;
+  }
+}
+
+// 16-byte stores for the aligned bulk of a fill.
+__global__ void fill_kernel_x4(uint4 *p, int64_t n16, uint4 v) {
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (; i < n16; i += stride)
+    p[i] = v;
+}
+
+} // namespace
+
+void set_last_error(const std::string &msg) { g_last_error = msg; }
+
+void ensure_init() {
+  Runtime &r = rt();
+  if (r.initialised)
+    return;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    fail(NT_ERR_RUNTIME, "no HIP device available");
+  }
+  NT_HIP_CHECK(hipSetDevice(0));
+  hipDeviceProp_t prop;
+  NT_HIP_CHECK(hipGetDeviceProperties(&prop, 0));
+  r.cu_count = prop.multiProcessorCount;
+  // Default priority, non-blocking w.r.t. the legacy null stream.
+  NT_HIP_CHECK(hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking));
+  r.available = true;
+  r.initialised = true;
+}
+
+hipStream_t stream() { return rt().stream; }
+int device_cu_count() { return rt().cu_count; }
+void *device_alloc(size_t nbytes) { return allocator().alloc(nbytes); }
+void device_free(void *p) { allocator().free(p); }
+
+JointLayout coalesce(const nt_view *const *ops, int nops) {
+  JointLayout L;
+  L.strides.resize(nops);
+  const nt_view *ref = ops[0];
+  // Keep dims of size != 1 (a size-1 dim never moves the index).
+  int nd = 0;
+  for (int d = 0; d < ref->ndim; ++d) {
+    if (ref->shape[d] == 1)
+      continue;
+    L.shape[nd] = ref->shape[d];
+    for (int k = 0; k < nops; ++k)
+      L.strides[k][nd] = ops[k]->strides[d];
+    ++nd;
+  }
+  // Merge dim d into d-1 when, for every operand, stepping the outer dim is
+  // the same as running off the end of the inner one.
+  int out = 0;
+  for (int d = 0; d < nd; ++d) {
+    if (out > 0) {
+      bool mergeable = true;
+      for (int k = 0; k < nops; ++k)
+        if (L.strides[k][out - 1] != L.strides[k][d] * L.shape[d]) {
+          mergeable = false;
+          break;
+        }
+      if (mergeable) {
+        L.shape[out - 1] *= L.shape[d];
+        for (int k = 0; k < nops; ++k)
+          L.strides[k][out - 1] = L.strides[k][d];
+        continue;
+      }
+    }
+    L.shape[out] = L.shape[d];
+    for (int k = 0; k < nops; ++k)
+      L.strides[k][out] = L.strides[k][d];
+    ++out;
+  }
+  L.ndim = out;
+  return L;
+}
+
+} // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_init(void) {
+  return guard([] {});
+}
+
+int nt_is_available(int *available) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess)
+    (void)hipGetLastError();
+  if (available)
+    *available = (e == hipSuccess && n > 0) ? 1 : 0;
+  return NT_OK;
+}
+
+int nt_sync(void) {
+  return guard([] { NT_HIP_CHECK(hipStreamSynchronize(stream())); });
+}
+
+const char *nt_last_error(void) { return g_last_error.c_str(); }
+
+int nt_malloc(void **ptr, size_t nbytes) {
+  return guard([&] {
+    if (!ptr)
+      fail(NT_ERR_RUNTIME, "nt_malloc: null out pointer");
+    *ptr = allocator().alloc(nbytes);
+  });
+}
+
+int nt_free(void *ptr) {
+  return guard([&] {
+    if (ptr)
+      allocator().free(ptr);
+  });
+}
+
+int nt_empty_cache(void) {
+  return guard([] { allocator().release_cache(); });
+}
+
+int nt_memory_stats(size_t *bytes_in_use, size_t *bytes_cached) {
+  return guard([&] {
+    if (bytes_in_use)
+      *bytes_in_use = allocator().bytes_in_use;
+    if (bytes_cached)
+      *bytes_cached = allocator().bytes_cached;
+  });
+}
+
+int nt_memcpy_h2d(void *dst, const void *src, size_t nbytes) {
+  return guard([&] {
+    if (nbytes == 0)
+      return;
+    NT_HIP_CHECK(
+        hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, stream()));
+    // The source is pageable caller memory that may be reused on return.
+    NT_HIP_CHECK(hipStreamSynchronize(stream()));
+  });
+}
+
+int nt_memcpy_d2h(void *dst, const void *src, size_t nbytes) {
+  return guard([&] {
+    if (nbytes == 0)
+      return;
+    NT_HIP_CHECK(
+        hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, stream()));
+    NT_HIP_CHECK(hipStreamSynchronize(stream()));
+  });
+}
+
+int nt_memcpy_d2d(void *dst, const void *src, size_t nbytes) {
+  return guard([&] {
+    if (nbytes == 0)
+      return;
+    NT_HIP_CHECK(
+        hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, stream()));
+  });
+}
+
+int nt_fill(void *data, int32_t dtype, int64_t n, double value) {
+  return guard([&] {
+    if (n < 0)
+      fail(NT_ERR_RUNTIME, "nt_fill: negative size");
+    if (n == 0)
+      return;
+    uint64_t pattern = 0;
+    size_t es = dtype_size(dtype);
+    dispatch_all(dtype, [&]<class T>() {
+      T v;
+      if constexpr (std::is_same_v<T, bool>)
+        v = (value != 0.0);
+      else
+        v = static_cast<T>(value);
+      std::memcpy(&pattern, &v, sizeof(T));
+    });
+    // Replicate the element into a 16-byte word for the bulk of the fill.
+    uint8_t word[16];
+    for (int i = 0; i < 16; ++i)
+      word[i] = reinterpret_cast<uint8_t *>(&pattern)[i % es];
+    uint4 v4;
+    std::memcpy(&v4, word, 16);
+    uint8_t *p = static_cast<uint8_t *>(data);
+    if (reinterpret_cast<uintptr_t>(p) % es != 0)
+      fail(NT_ERR_RUNTIME, "nt_fill: pointer not aligned to the element size");
+    int64_t nbytes = n * int64_t(es);
+    int64_t head = 0;
+    uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+    if (addr % 16 != 0)
+      head = std::min<int64_t>(nbytes, (16 - addr % 16));
+    head -= head % int64_t(es); // element aligned (allocations are aligned)
+    int64_t n16 = (nbytes - head) / 16;
+    int64_t tail_start = head + n16 * 16;
+    int threads = 256;
+    if (head > 0) {
+      fill_kernel_bytes<<<1, threads, 0, stream()>>>(p, head / int64_t(es),
+                                                     pattern, int(es));
+      NT_LAUNCH_CHECK();
+    }
+    if (n16 > 0) {
+      int64_t blocks = std::min<int64_t>((n16 + threads - 1) / threads,
+                                         int64_t(device_cu_count()) * 16);
+      fill_kernel_x4<<<dim3(unsigned(blocks)), threads, 0, stream()>>>(
+          reinterpret_cast<uint4 *>(p + head), n16, v4);
+      NT_LAUNCH_CHECK();
+    }
+    if (tail_start < nbytes) {
+      fill_kernel_bytes<<<1, threads, 0, stream()>>>(
+          p + tail_start, (nbytes - tail_start) / int64_t(es), pattern,
+          int(es));
+      NT_LAUNCH_CHECK();
+    }
+  });
+}
+
+int nt_manual_seed(uint64_t seed) {
+  try {
+    host_rng().seed(seed);
+  } catch (...) {
+    return NT_ERR_RUNTIME;
+  }
+  return NT_OK;
+}
+
+int nt_host_uniform(void *host_out, int32_t dtype, int64_t n, double low,
+                    double high) {
+  // No device needed: this is the reference's host-side generator.
+  try {
+    if (dtype == NT_FLOAT32) {
+      std::uniform_real_distribution<float> dist{float(low), float(high)};
+      float *o = static_cast<float *>(host_out);
+      for (int64_t i = 0; i < n; ++i)
+        o[i] = dist(host_rng());
+    } else if (dtype == NT_FLOAT64) {
+      std::uniform_real_distribution<double> dist{low, high};
+      double *o = static_cast<double *>(host_out);
+      for (int64_t i = 0; i < n; ++i)
+        o[i] = dist(host_rng());
+    } else {
+      set_last_error("nt_host_uniform: float dtype required");
+      return NT_ERR_VALUE;
+    }
+  } catch (const std::exception &e) {
+    set_last_error(e.what());
+    return NT_ERR_RUNTIME;
+  }
+  return NT_OK;
+}
+
+int nt_event_create(void **ev) {
+  return guard([&] {
+    hipEvent_t e;
+    NT_HIP_CHECK(hipEventCreate(&e));
+    *ev = reinterpret_cast<void *>(e);
+  });
+}
+
+int nt_event_record(void *ev) {
+  return guard([&] {
+    NT_HIP_CHECK(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), stream()));
+  });
+}
+
+int nt_event_elapsed_ms(void *start, void *end, float *ms) {
+  return guard([&] {
+    NT_HIP_CHECK(hipEventSynchronize(reinterpret_cast<hipEvent_t>(end)));
+    NT_HIP_CHECK(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                     reinterpret_cast<hipEvent_t>(end)));
+  });
+}
+
+int nt_event_destroy(void *ev) {
+  return guard([&] {
+    NT_HIP_CHECK(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+  });
+}
+
+} // extern "C"

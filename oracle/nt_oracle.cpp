@@ -1,0 +1,436 @@
+// nt_oracle -- CPU restatement of the reference's CPU kernels.  TEST
+// INFRASTRUCTURE ONLY: used by tests/, by __graft_entry__.smoke() and by the
+// cpu_baseline leg of bench.py as the checker and the CPU baseline.  Nothing
+// in the nanotorch_amd package loads it.
+//
+// Every loop follows the reference's CPU code path element for element:
+//   unary     src/cpp/ops/unary_ops.cu:6-17 (loop), :40-58 (int_pow/PowOp),
+//             :101-107 (ops: exp, log, neg, relu, sqrt, tanh, sigmoid)
+//   binary    src/cpp/ops/binary_ops.cu:6-20 (loop), :107-113 (ops)
+//   in-place  src/cpp/ops/inplace_ops.cu:6-16 (loop), :75-79 (ops)
+//   cast      src/cpp/storage.cpp:47-65 (bool: s ? 1 : 0, else static_cast)
+//   reduce    src/cpp/ops/reduction_ops.cu:8-76 (MatItem, combine ops,
+//             sequential loop), :183-233 (keep/drop views)
+//   matmul    src/cpp/ops/matmul.cu:21-57 (sequential k dot product)
+//   unravel   src/cpp/tensor_view.cuh:42-52
+// The logical index walks row-major order; outputs are contiguous.
+// Built with -O3 -ffp-contract=off and no fast-math, so each + - * / is one
+// IEEE rounding as in the reference, and the std:: math calls resolve to the
+// host libm exactly as the reference's CPU path does.
+//
+// or_matmul_omp computes each output with the same sequential k loop, only
+// spreading outputs over OpenMP threads: bit-identical to or_matmul.
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+extern "C" {
+typedef struct or_view {
+  void *data;
+  int64_t offset;
+  int32_t dtype; // 0 bool, 1 int32, 2 int64, 3 float32, 4 float64
+  int32_t ndim;
+  int64_t shape[8];
+  int64_t strides[8];
+} or_view;
+}
+
+namespace {
+
+thread_local std::string g_err;
+
+template <class F> int guard(F &&f) {
+  try {
+    f();
+    return 0;
+  } catch (const std::invalid_argument &e) {
+    g_err = e.what();
+    return 2;
+  } catch (const std::exception &e) {
+    g_err = e.what();
+    return 1;
+  }
+}
+
+template <class F> void dispatch_all(int dt, F &&f) {
+  switch (dt) {
+  case 0:
+    return f.template operator()<bool>();
+  case 1:
+    return f.template operator()<int32_t>();
+  case 2:
+    return f.template operator()<int64_t>();
+  case 3:
+    return f.template operator()<float>();
+  case 4:
+    return f.template operator()<double>();
+  }
+  throw std::invalid_argument("Unknown dtype.");
+}
+template <class F> void dispatch_float(int dt, F &&f) {
+  if (dt == 3)
+    return f.template operator()<float>();
+  if (dt == 4)
+    return f.template operator()<double>();
+  throw std::invalid_argument("Invalid dtype.");
+}
+template <class F> void dispatch_arith(int dt, F &&f) {
+  switch (dt) {
+  case 1:
+    return f.template operator()<int32_t>();
+  case 2:
+    return f.template operator()<int64_t>();
+  case 3:
+    return f.template operator()<float>();
+  case 4:
+    return f.template operator()<double>();
+  }
+  throw std::invalid_argument("Invalid dtype.");
+}
+
+int64_t numel(const or_view &v) {
+  int64_t n = 1;
+  for (int i = 0; i < v.ndim; ++i)
+    n *= v.shape[i];
+  return n;
+}
+
+// tensor_view.cuh:42-52
+int64_t unravel(int64_t i, const or_view &v) {
+  int64_t idx = v.offset;
+  for (int64_t j = v.ndim - 1; j >= 0; --j) {
+    int64_t coord = i % v.shape[j];
+    i /= v.shape[j];
+    idx += coord * v.strides[j];
+  }
+  return idx;
+}
+
+void same_shape(const or_view &a, const or_view &b) {
+  if (a.ndim != b.ndim)
+    throw std::runtime_error("shape mismatch");
+  for (int i = 0; i < a.ndim; ++i)
+    if (a.shape[i] != b.shape[i])
+      throw std::runtime_error("shape mismatch");
+}
+
+template <class T> T int_pow(T a, T n) {
+  T r = 1;
+  while (n > 0) {
+    if (n & 1)
+      r *= a;
+    a *= a;
+    n >>= 1;
+  }
+  return r;
+}
+
+template <class T> T unary_apply(int op, T a, T e) {
+  switch (op) {
+  case 0:
+    if constexpr (std::is_floating_point_v<T>)
+      return std::exp(a);
+    break;
+  case 1:
+    if constexpr (std::is_floating_point_v<T>)
+      return std::log(a);
+    break;
+  case 2:
+    return -a;
+  case 3:
+    return (a >= 0) ? a : 0;
+  case 4:
+    if constexpr (std::is_floating_point_v<T>)
+      return std::sqrt(a);
+    break;
+  case 5:
+    if constexpr (std::is_floating_point_v<T>)
+      return std::tanh(a);
+    break;
+  case 6:
+    if constexpr (std::is_floating_point_v<T>)
+      return T(1) / (T(1) + std::exp(-a));
+    break;
+  case 7:
+    if constexpr (std::is_integral_v<T>)
+      return int_pow(a, e);
+    else
+      return std::pow(a, e);
+  }
+  throw std::invalid_argument("Invalid dtype.");
+}
+
+template <class T> T binary_apply(int op, T a, T b) {
+  switch (op) {
+  case 0:
+    return a + b;
+  case 1:
+    return a - b;
+  case 2:
+    return a * b;
+  case 3:
+    return a / b;
+  }
+  throw std::invalid_argument("unknown op");
+}
+
+// reduction_ops.cu:8-50
+template <class O> struct MatItem {
+  int64_t idx;
+  O value;
+};
+
+template <class O> MatItem<O> combine(int op, MatItem<O> a, MatItem<O> b) {
+  if (op == 0)
+    return MatItem<O>{-1, static_cast<O>(a.value + b.value)};
+  if (op == 1 || op == 3) // max / argmax
+    return (a.value > b.value || (a.value == b.value && a.idx < b.idx)) ? a : b;
+  return (a.value < b.value || (a.value == b.value && a.idx < b.idx)) ? a : b;
+}
+
+template <class O> MatItem<O> neutral(int op) {
+  if (op == 0)
+    return MatItem<O>{-1, O(0)};
+  if (op == 1 || op == 3)
+    return MatItem<O>{std::numeric_limits<int64_t>::max(),
+                      std::numeric_limits<O>::lowest()};
+  return MatItem<O>{std::numeric_limits<int64_t>::max(),
+                    std::numeric_limits<O>::max()};
+}
+
+} // namespace
+
+extern "C" {
+
+const char *or_last_error(void) { return g_err.c_str(); }
+
+int or_has_openmp(void) {
+#ifdef _OPENMP
+  return 1;
+#else
+  return 0;
+#endif
+}
+
+int or_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+// out: contiguous, same dtype as x.
+int or_unary(int32_t op, const or_view *x, double scalar, void *out) {
+  return guard([&] {
+    auto run = [&]<class T>() {
+      const T *in = static_cast<const T *>(x->data);
+      T *o = static_cast<T *>(out);
+      const T e = static_cast<T>(scalar);
+      const int64_t n = numel(*x);
+      for (int64_t i = 0; i < n; ++i)
+        o[i] = unary_apply<T>(op, in[unravel(i, *x)], e);
+    };
+    if (op == 2 || op == 3 || op == 7)
+      dispatch_arith(x->dtype, run);
+    else
+      dispatch_float(x->dtype, run);
+  });
+}
+
+// op 0..3 arithmetic (out dtype = a dtype), 4 ==, 5 >, 6 >= (out bool).
+int or_binary(int32_t op, const or_view *a, const or_view *b, void *out) {
+  return guard([&] {
+    same_shape(*a, *b);
+    if (a->dtype != b->dtype)
+      throw std::runtime_error("dtype mismatch");
+    const int64_t n = numel(*a);
+    auto run = [&]<class T>() {
+      const T *pa = static_cast<const T *>(a->data);
+      const T *pb = static_cast<const T *>(b->data);
+      if (op >= 4) {
+        bool *o = static_cast<bool *>(out);
+        for (int64_t i = 0; i < n; ++i) {
+          const T x = pa[unravel(i, *a)], y = pb[unravel(i, *b)];
+          o[i] = op == 4 ? (x == y) : op == 5 ? (x > y) : (x >= y);
+        }
+      } else {
+        T *o = static_cast<T *>(out);
+        for (int64_t i = 0; i < n; ++i)
+          o[i] = static_cast<T>(
+              binary_apply<T>(op, pa[unravel(i, *a)], pb[unravel(i, *b)]));
+      }
+    };
+    if (op == 3)
+      dispatch_arith(a->dtype, run);
+    else
+      dispatch_all(a->dtype, run);
+  });
+}
+
+// out = out (op) other in place; op 0..3, 7 = copy.
+int or_inplace(int32_t op, const or_view *out, const or_view *other) {
+  return guard([&] {
+    same_shape(*out, *other);
+    if (out->dtype != other->dtype)
+      throw std::runtime_error("dtype mismatch");
+    const int64_t n = numel(*out);
+    auto run = [&]<class T>() {
+      T *po = static_cast<T *>(out->data);
+      const T *px = static_cast<const T *>(other->data);
+      for (int64_t i = 0; i < n; ++i) {
+        const int64_t io = unravel(i, *out);
+        const T b = px[unravel(i, *other)];
+        po[io] = op == 7 ? b : static_cast<T>(binary_apply<T>(op, po[io], b));
+      }
+    };
+    if (op == 3)
+      dispatch_arith(out->dtype, run);
+    else
+      dispatch_all(out->dtype, run);
+  });
+}
+
+// dst (contiguous, dtype dst_dtype) = cast(src view).
+int or_cast(const or_view *src, int32_t dst_dtype, void *dst) {
+  return guard([&] {
+    const int64_t n = numel(*src);
+    dispatch_all(src->dtype, [&]<class S>() {
+      dispatch_all(dst_dtype, [&]<class D>() {
+        const S *s = static_cast<const S *>(src->data);
+        D *d = static_cast<D *>(dst);
+        for (int64_t i = 0; i < n; ++i) {
+          const S v = s[unravel(i, *src)];
+          if constexpr (std::is_same_v<D, bool>)
+            d[i] = v ? D{1} : D{0};
+          else
+            d[i] = static_cast<D>(v);
+        }
+      });
+    });
+  });
+}
+
+// op 0 sum (accumulation dtype out_dtype), 1 max, 2 min (out dtype = x),
+// 3 argmax, 4 argmin (int64).  out contiguous over the kept axes.
+int or_reduce(int32_t op, const or_view *x, const int64_t *axes, int32_t naxes,
+              int32_t out_dtype, void *out) {
+  return guard([&] {
+    std::vector<bool> drop(x->ndim, false);
+    or_view keep{}, dv{};
+    keep.offset = x->offset;
+    for (int i = 0; i < naxes; ++i) {
+      if (axes[i] < 0 || axes[i] >= x->ndim || drop[axes[i]])
+        throw std::runtime_error("bad axes");
+      drop[axes[i]] = true;
+      dv.shape[dv.ndim] = x->shape[axes[i]];
+      dv.strides[dv.ndim] = x->strides[axes[i]];
+      dv.ndim++;
+    }
+    for (int d = 0; d < x->ndim; ++d)
+      if (!drop[d]) {
+        keep.shape[keep.ndim] = x->shape[d];
+        keep.strides[keep.ndim] = x->strides[d];
+        keep.ndim++;
+      }
+    const int64_t nk = numel(keep), nd = numel(dv);
+    if (op == 1 || op == 2)
+      out_dtype = x->dtype;
+    dispatch_all(x->dtype, [&]<class T>() {
+      const T *in = static_cast<const T *>(x->data);
+      auto body = [&]<class O>() {
+        for (int64_t i = 0; i < nk; ++i) {
+          const int64_t base = unravel(i, keep);
+          MatItem<O> acc = neutral<O>(op);
+          for (int64_t j = 0; j < nd; ++j)
+            acc = combine<O>(
+                op, acc,
+                MatItem<O>{j, static_cast<O>(in[base + unravel(j, dv)])});
+          if (op >= 3)
+            static_cast<int64_t *>(out)[i] = acc.idx;
+          else
+            static_cast<O *>(out)[i] = acc.value;
+        }
+      };
+      if (op == 0)
+        dispatch_arith(out_dtype, body);
+      else
+        body.template operator()<T>();
+    });
+  });
+}
+
+static int matmul_impl(const or_view *a, const or_view *b, void *out,
+                       bool parallel) {
+  return guard([&] {
+    if (a->dtype != b->dtype || a->ndim != b->ndim || a->ndim < 2)
+      throw std::invalid_argument("matmul: bad operands");
+    const int nd = a->ndim;
+    for (int d = 0; d < nd - 2; ++d)
+      if (a->shape[d] != b->shape[d])
+        throw std::invalid_argument("Invalid broacast shapes.");
+    const int64_t M = a->shape[nd - 2], K = a->shape[nd - 1],
+                  N = b->shape[nd - 1];
+    if (b->shape[nd - 2] != K)
+      throw std::invalid_argument("Invalid matmul shape.");
+    std::vector<int64_t> oshape(a->shape, a->shape + nd);
+    oshape[nd - 1] = N;
+    int64_t total = 1;
+    for (auto s : oshape)
+      total *= s;
+    dispatch_arith(a->dtype, [&]<class T>() {
+      const T *A = static_cast<const T *>(a->data);
+      const T *B = static_cast<const T *>(b->data);
+      T *C = static_cast<T *>(out);
+      auto one = [&](int64_t idx) {
+        // loc = row-major coordinates of output idx (matmul.cu:31-56)
+        int64_t loc[8];
+        int64_t r = idx;
+        for (int d = nd - 1; d >= 0; --d) {
+          loc[d] = r % oshape[d];
+          r /= oshape[d];
+        }
+        T acc = static_cast<T>(0.0);
+        for (int64_t c = 0; c < K; ++c) {
+          int64_t i1 = a->offset + c * a->strides[nd - 1] +
+                       loc[nd - 2] * a->strides[nd - 2];
+          int64_t i2 = b->offset + c * b->strides[nd - 2] +
+                       loc[nd - 1] * b->strides[nd - 1];
+          for (int d = 0; d < nd - 2; ++d) {
+            i1 += a->strides[d] * loc[d];
+            i2 += b->strides[d] * loc[d];
+          }
+          acc += A[i1] * B[i2];
+        }
+        C[idx] = acc;
+      };
+      if (parallel) {
+#pragma omp parallel for schedule(static)
+        for (int64_t idx = 0; idx < total; ++idx)
+          one(idx);
+      } else {
+        for (int64_t idx = 0; idx < total; ++idx)
+          one(idx);
+      }
+    });
+  });
+}
+
+int or_matmul(const or_view *a, const or_view *b, void *out) {
+  return matmul_impl(a, b, out, false);
+}
+
+int or_matmul_omp(const or_view *a, const or_view *b, void *out) {
+  return matmul_impl(a, b, out, true);
+}
+
+} // extern "C"

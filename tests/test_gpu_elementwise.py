@@ -1,0 +1,285 @@
+"""Elementwise family on the GPU against the oracle (reference CPU loops).
+
+Bar: bit-exact for +, -, *, /, neg, relu, sqrt, comparisons, casts and for
+the fused backward chains given the same saved tensors (their only non-IEEE
+step, pow(v, 2) / pow(v, -1), equals v*v / 1/v in glibc, checked on the CPU
+in test_oracle_pinning.py); rel 1e-6 for exp/log/tanh/sigmoid/pow forward
+and the pow backward (device libm vs host libm, a few ulps).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import assert_bitexact, assert_rel, dev, dev_T, host, rng, seed_of
+
+import nanotorch_amd as nt
+from nanotorch_amd import _kernels as K
+from nanotorch_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+UNARY = [
+    ("exp", _lib.EXP, O.EXP, (-4, 4), False),
+    ("log", _lib.LOG, O.LOG, (0.1, 4), False),
+    ("neg", _lib.NEG, O.NEG, (-4, 4), True),
+    ("relu", _lib.RELU, O.RELU, None, True),
+    ("sqrt", _lib.SQRT, O.SQRT, (0.1, 4), True),
+    ("tanh", _lib.TANH, O.TANH, None, False),
+    ("sigmoid", _lib.SIGMOID, O.SIGMOID, None, False),
+    ("pow", _lib.POW, O.POW, (0.1, 4), False),
+]
+
+BINARY = [("add", _lib.ADD, O.ADD), ("sub", _lib.SUB, O.SUB),
+          ("mul", _lib.MUL, O.MUL), ("div", _lib.DIV, O.DIV)]
+
+
+def _inputs(r, dom, shape, dtype=np.float32):
+    if dom is None:
+        return r.standard_normal(shape).astype(dtype)
+    return r.uniform(dom[0], dom[1], shape).astype(dtype)
+
+
+def _mk(a, layout):
+    return dev(a) if layout == "contig" else dev_T(a)
+
+
+@pytest.mark.parametrize("layout", ["contig", "transposed"])
+@pytest.mark.parametrize("shape", [(1, 1), (7, 13), (64, 64), (129, 300), (256, 1024)])
+@pytest.mark.parametrize("name,op,oop,dom,exact", UNARY)
+def test_unary_forward(gpu, name, op, oop, dom, exact, shape, layout):
+    r = rng(seed_of(name, shape))
+    a = _inputs(r, dom, shape)
+    e = 2.5 if name == "pow" else 0.0
+    x = _mk(a, layout)
+    got = host(nt.Tensor._new_contiguous(K.unary(op, x, e), x.shape))
+    want = O.unary(oop, a, e)
+    if exact:
+        assert_bitexact(got, want, name)
+    else:
+        assert_rel(got, want, 1e-6, name)
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+def test_unary_integer(gpu, dtype):
+    r = rng(3)
+    a = r.integers(-50, 50, (33, 17)).astype(dtype)
+    for op, oop, e in ((_lib.NEG, O.NEG, 0), (_lib.RELU, O.RELU, 0), (_lib.POW, O.POW, 3)):
+        x = dev(a)
+        got = host(nt.Tensor._new_contiguous(K.unary(op, x, e), x.shape))
+        assert_bitexact(got, O.unary(oop, a, e), f"int op {op}")
+
+
+def test_unary_float64(gpu):
+    r = rng(4)
+    a = r.uniform(0.1, 4, (40, 50))
+    for op, oop in ((_lib.EXP, O.EXP), (_lib.LOG, O.LOG), (_lib.SQRT, O.SQRT),
+                    (_lib.TANH, O.TANH), (_lib.SIGMOID, O.SIGMOID)):
+        got = host(nt.Tensor._new_contiguous(K.unary(op, dev(a), 0.0), a.shape))
+        assert_rel(got, O.unary(oop, a), 1e-14, f"f64 op {op}")
+
+
+def test_unary_dtype_errors(gpu):
+    with pytest.raises(ValueError):
+        K.unary(_lib.EXP, dev(np.arange(4, dtype=np.int64)))
+    with pytest.raises(ValueError):
+        K.unary(_lib.NEG, dev(np.array([True, False])))
+
+
+@pytest.mark.parametrize("layout", ["contig", "transposed", "mixed"])
+@pytest.mark.parametrize("shape", [(1, 1), (5, 7), (64, 64), (130, 257), (512, 384)])
+@pytest.mark.parametrize("name,op,oop", BINARY)
+def test_binary_forward(gpu, name, op, oop, shape, layout):
+    r = rng(seed_of(name, shape, layout))
+    a = r.standard_normal(shape).astype(np.float32)
+    b = (r.uniform(0.5, 2, shape) if name == "div" else r.standard_normal(shape)).astype(
+        np.float32
+    )
+    xa = _mk(a, "contig" if layout == "mixed" else layout)
+    xb = _mk(b, "transposed" if layout == "mixed" else layout)
+    got = host(nt.Tensor._new_contiguous(K.binary(op, xa, xb), shape))
+    assert_bitexact(got, O.binary(oop, a, b), name)
+
+
+@pytest.mark.parametrize("dtype", [np.bool_, np.int32, np.int64, np.float64])
+def test_binary_other_dtypes(gpu, dtype):
+    r = rng(5)
+    if dtype == np.bool_:
+        a = r.integers(0, 2, (17, 19)).astype(bool)
+        b = r.integers(0, 2, (17, 19)).astype(bool)
+        ops = [(_lib.ADD, O.ADD), (_lib.SUB, O.SUB), (_lib.MUL, O.MUL)]
+    else:
+        a = r.integers(-100, 100, (17, 19)).astype(dtype)
+        b = r.integers(1, 100, (17, 19)).astype(dtype)
+        ops = [(_lib.ADD, O.ADD), (_lib.SUB, O.SUB), (_lib.MUL, O.MUL), (_lib.DIV, O.DIV)]
+    for op, oop in ops:
+        got = host(nt.Tensor._new_contiguous(K.binary(op, dev(a), dev(b)), a.shape))
+        assert_bitexact(got, O.binary(oop, a, b), f"{dtype} {op}")
+    if dtype == np.bool_:
+        with pytest.raises(ValueError):
+            K.binary(_lib.DIV, dev(a), dev(b))
+
+
+@pytest.mark.parametrize("op,oop", [(_lib.EQ, O.EQ), (_lib.GT, O.GT), (_lib.GE, O.GE)])
+def test_compare(gpu, op, oop):
+    r = rng(6)
+    a = r.integers(-3, 3, (65, 33)).astype(np.float32)
+    b = r.integers(-3, 3, (65, 33)).astype(np.float32)
+    got = host(nt.Tensor._new_contiguous(K.binary(op, dev(a), dev_T(b)), a.shape))
+    assert_bitexact(got, O.binary(oop, a, b), "compare")
+
+
+def test_broadcast_and_strided_views(gpu):
+    r = rng(7)
+    a = r.standard_normal((6, 40, 50)).astype(np.float32)
+    bias = r.standard_normal((50,)).astype(np.float32)
+    col = r.standard_normal((40, 1)).astype(np.float32)
+    x = dev(a)
+    # row broadcast (bias), column broadcast, strided slices, 3-D transpose
+    for other, onp in (
+        (dev(bias).expand(6, 40, 50), np.broadcast_to(bias, a.shape)),
+        (dev(col).expand(6, 40, 50), np.broadcast_to(col, a.shape)),
+    ):
+        got = host(nt.Tensor._new_contiguous(K.binary(_lib.ADD, x, other), a.shape))
+        assert_bitexact(got, O.binary(O.ADD, a, np.ascontiguousarray(onp)), "bcast")
+    big = r.standard_normal((6, 40, 100)).astype(np.float32)
+    xs = dev(big)[:, :, ::2]
+    got = host(nt.Tensor._new_contiguous(K.unary(_lib.NEG, xs), xs.shape))
+    assert_bitexact(got, -big[:, :, ::2], "strided")
+    xt = dev(a).transpose(0, 2)
+    got = host(nt.Tensor._new_contiguous(K.unary(_lib.RELU, xt), xt.shape))
+    assert_bitexact(got, O.unary(O.RELU, np.ascontiguousarray(a.transpose(2, 1, 0))), "3d-T")
+
+
+@pytest.mark.parametrize("src,dst", [(np.float32, np.float64), (np.float64, np.float32),
+                                     (np.float32, np.int64), (np.int64, np.float32),
+                                     (np.float32, np.bool_), (np.bool_, np.float32),
+                                     (np.int64, np.int32), (np.int32, np.bool_)])
+def test_cast(gpu, src, dst):
+    r = rng(8)
+    a = (r.standard_normal((31, 29)) * 10).astype(src)
+    if src == np.bool_:
+        a = r.integers(0, 2, (31, 29)).astype(bool)
+    st = K.cast(dev(a)._storage, nt.Tensor(np.zeros(1, dtype=dst)).dtype)
+    got = host(nt.Tensor._new_contiguous(st, a.shape))
+    assert_bitexact(got, O.cast(a, dst), f"cast {src}->{dst}")
+
+
+def test_inplace_and_copy(gpu):
+    r = rng(9)
+    a = r.standard_normal((70, 90)).astype(np.float32)
+    b = r.standard_normal((90, 70)).astype(np.float32)
+    for op, oop in ((_lib.ADD, O.ADD), (_lib.SUB, O.SUB), (_lib.MUL, O.MUL), (_lib.DIV, O.DIV)):
+        x = dev(a)
+        y = dev(b).T  # transposed operand
+        v0 = x.version
+        K.inplace(op, x, y)
+        want = a.copy()
+        O.inplace(oop, want, b.T)
+        assert_bitexact(host(x), want, f"inplace {op}")
+        assert x.version == v0 + 1
+    # in place through a transposed view of the output
+    x = dev(np.ascontiguousarray(a.T))
+    K.inplace(_lib.ADD, x.T, dev(a))
+    assert_bitexact(host(x), np.ascontiguousarray((a + a).T), "inplace via view")
+
+
+def test_equals(gpu):
+    a = np.arange(12, dtype=np.float32).reshape(3, 4)
+    assert dev(a).equals(dev(a.copy()))
+    b = a.copy()
+    b[2, 3] = -1
+    assert not dev(a).equals(dev(b))
+    assert dev(a).T.equals(dev(np.ascontiguousarray(a.T)))
+
+
+# --------------------------------------------------------------- backward
+
+UNARY_BWD = [
+    ("neg", _lib.NEG, None, lambda g, s: O.bwd_neg(g), (-4, 4), "none"),
+    ("exp", _lib.EXP, O.EXP, O.bwd_exp, (-4, 4), "out"),
+    ("log", _lib.LOG, O.LOG, O.bwd_log, (0.1, 4), "in"),
+    ("sqrt", _lib.SQRT, O.SQRT, O.bwd_sqrt, (0.1, 4), "out"),
+    ("tanh", _lib.TANH, O.TANH, O.bwd_tanh, None, "out"),
+    ("sigmoid", _lib.SIGMOID, O.SIGMOID, O.bwd_sigmoid, None, "out"),
+    ("relu", _lib.RELU, O.RELU, O.bwd_relu, None, "out"),
+    ("pow", _lib.POW, O.POW, lambda g, x: O.bwd_pow(g, x, 2.5), (0.1, 4), "in"),
+]
+
+
+@pytest.mark.parametrize("acc", [False, True])
+@pytest.mark.parametrize("layout", ["contig", "transposed"])
+@pytest.mark.parametrize("name,op,oop,chain,dom,saved", UNARY_BWD)
+def test_unary_backward_kernel(gpu, name, op, oop, chain, dom, saved, layout, acc):
+    """Kernel parity: feed the oracle's saved tensor to the fused kernel."""
+    r = rng(seed_of(name, layout, acc))
+    shape = (130, 200)
+    x = _inputs(r, dom, shape)
+    g = r.standard_normal(shape).astype(np.float32)
+    e = 2.5 if name == "pow" else 0.0
+    s = None if saved == "none" else (x if saved == "in" else O.unary(oop, x, e))
+    want = chain(g, s)
+    old = r.standard_normal(shape).astype(np.float32)
+    if acc:
+        want = O.accumulate(old, want)
+    sv = None if s is None else _mk(s, layout)
+    if acc:
+        tgt = _mk(old, layout)
+        K.unary_bwd(op, dev(g), sv, e, tgt)
+        got = host(tgt)
+    else:
+        st = K.unary_bwd(op, dev(g), sv, e, None)
+        got = host(nt.Tensor._new_contiguous(st, shape))
+    if name == "pow":
+        assert_rel(got, want, 1e-6, name)
+    else:
+        assert_bitexact(got, want, name)
+
+
+@pytest.mark.parametrize("acc", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("need", [(True, True), (True, False), (False, True)])
+@pytest.mark.parametrize("name,op,oop", BINARY)
+def test_binary_backward_kernel(gpu, name, op, oop, need, acc):
+    r = rng(seed_of(name, need, acc))
+    shape = (97, 131)
+    a = r.standard_normal(shape).astype(np.float32)
+    b = (r.uniform(0.5, 2, shape) if name == "div" else r.standard_normal(shape)).astype(np.float32)
+    g = r.standard_normal(shape).astype(np.float32)
+    ga_w, gb_w = O.bwd_binary(oop, g, a, b)
+    olds = [r.standard_normal(shape).astype(np.float32) for _ in range(2)]
+    tg = [dev(olds[0]) if acc[0] else None, dev_T(olds[1]) if acc[1] else None]
+    sa, sb = K.binary_bwd(op, dev(g), dev_T(a), dev(b), need[0], tg[0], need[1], tg[1])
+    for i, (n, s_, w) in enumerate(((need[0], sa, ga_w), (need[1], sb, gb_w))):
+        if not n:
+            continue
+        if acc[i]:
+            got = host(tg[i])
+            w = O.accumulate(olds[i], w)
+        else:
+            got = host(nt.Tensor._new_contiguous(s_, shape))
+        assert_bitexact(got, w, f"{name} grad {i}")
+
+
+# ------------------------------------------------------------ config 2 size
+
+
+@pytest.mark.parametrize("layout", ["contig", "transposed"])
+def test_config2_full_size(gpu, layout):
+    """[4096, 4096] (2^24 elements): mul forward and fused backward
+    (accumulate), tanh forward, both layouts, against the oracle."""
+    r = rng(11)
+    shape = (4096, 4096)
+    a = r.standard_normal(shape).astype(np.float32)
+    b = r.standard_normal(shape).astype(np.float32)
+    g = r.standard_normal(shape).astype(np.float32)
+    xa, xb = _mk(a, layout), _mk(b, layout)
+    got = host(nt.Tensor._new_contiguous(K.binary(_lib.MUL, xa, xb), shape))
+    assert_bitexact(got, O.binary(O.MUL, a, b), "mul fwd 2^24")
+    old = r.standard_normal(shape).astype(np.float32)
+    tgt = dev(old)
+    K.binary_bwd(_lib.MUL, dev(g), xa, xb, True, tgt, False, None)
+    assert_bitexact(host(tgt), O.accumulate(old, O.binary(O.MUL, b, g)), "mul bwd 2^24")
+    got = host(nt.Tensor._new_contiguous(K.unary(_lib.TANH, xa), shape))
+    assert_rel(got, O.unary(O.TANH, a), 1e-6, "tanh 2^24")

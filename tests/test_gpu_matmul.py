@@ -1,0 +1,123 @@
+"""MatMulOp forward and both gradients on the GPU (fp32 MFMA) against the
+oracle's sequential dot products.
+
+Bar: |gpu - ref| <= 1e-4 * (|A|.|B|)_ij per element (a different fp32
+accumulation order), plus a normwise check.  Small problems are compared in
+full; the config shapes are compared on sampled output elements (each a
+full-length sequential dot product in the oracle).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import assert_bitexact, assert_rel, dev, dev_T, host, rng, seed_of
+
+import nanotorch_amd as nt
+from nanotorch_amd import _kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def _mm(x1, x2):
+    out_shape = tuple(x1.shape[:-2]) + (x1.shape[-2], x2.shape[-1])
+    return host(nt.Tensor._new_contiguous(K.matmul(x1, x2, out_shape), out_shape))
+
+
+def _check(got, a, b, what):
+    want = O.matmul(np.ascontiguousarray(a), np.ascontiguousarray(b), parallel=True)
+    scale = O.matmul(np.abs(a).astype(np.float64), np.abs(b).astype(np.float64), parallel=True)
+    assert_rel(got, want, 1e-4, what, scale=scale)
+    nrm = np.linalg.norm(got.astype(np.float64) - want) / max(np.linalg.norm(want), 1e-30)
+    assert nrm < 1e-5, (what, nrm)
+
+
+SHAPES = [(1, 1, 1), (2, 3, 4), (5, 7, 3), (32, 32, 32), (128, 128, 128), (129, 33, 130),
+          (257, 100, 63), (64, 1000, 96), (300, 257, 511), (1024, 512, 768)]
+
+
+@pytest.mark.parametrize("layout", ["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("M,K_,N", SHAPES)
+def test_matmul_layouts(gpu, M, K_, N, layout):
+    r = rng(seed_of(M, K_, N, layout))
+    a = r.standard_normal((M, K_)).astype(np.float32)
+    b = (r.standard_normal((K_, N)) / np.sqrt(K_)).astype(np.float32)
+    xa = dev_T(a) if layout[0] == "T" else dev(a)
+    xb = dev_T(b) if layout[1] == "T" else dev(b)
+    _check(_mm(xa, xb), a, b, f"{layout} {M}x{K_}x{N}")
+
+
+def test_matmul_generic_strides_and_batch(gpu):
+    r = rng(1)
+    a = r.standard_normal((3, 4 * 2)).astype(np.float32)
+    b = np.ones((4, 2), dtype=np.float32)
+    got = _mm(dev(np.arange(12, dtype=np.float32).reshape(3, 4))[:, ::2], dev(np.ones((2, 2), np.float32)))
+    assert_bitexact(got, np.array([[2, 2], [10, 10], [18, 18]], np.float32), "strided ::2")
+    # batched with a broadcast (stride-0) batch operand
+    a = r.standard_normal((4, 3, 37, 19)).astype(np.float32)
+    b = r.standard_normal((19, 23)).astype(np.float32)
+    xb = dev(b).expand(4, 3, 19, 23)
+    got = _mm(dev(a), xb)
+    _check(got, a, np.broadcast_to(b, (4, 3, 19, 23)), "batched+bcast")
+    del b
+
+
+def test_matmul_other_dtypes_exact(gpu):
+    """fp64 / int paths accumulate in k order like the reference: exact."""
+    r = rng(2)
+    for dt in (np.float64, np.int64, np.int32):
+        a = (r.standard_normal((33, 45)) * 10).astype(dt)
+        b = (r.standard_normal((45, 27)) * 10).astype(dt)
+        got = _mm(dev(a), dev_T(b))
+        assert_bitexact(got, O.matmul(a, b), f"{dt}")
+
+
+def test_matmul_accumulate(gpu):
+    r = rng(3)
+    a = r.standard_normal((200, 150)).astype(np.float32)
+    b = r.standard_normal((150, 170)).astype(np.float32)
+    old = r.standard_normal((200, 170)).astype(np.float32)
+    tgt = dev(old)
+    K.matmul_into(dev(a), dev(b), tgt, accumulate=True)
+    want = O.matmul(a, b) + old
+    scale = O.matmul(np.abs(a).astype(np.float64), np.abs(b).astype(np.float64)) + np.abs(old)
+    assert_rel(host(tgt), want, 1e-4, "accumulate", scale=scale)
+
+
+def _sampled_check(got, A, B, r, what, n=256):
+    """Compare n random output elements against sequential dot products."""
+    M, N = got.shape
+    ii = r.integers(0, M, n)
+    jj = r.integers(0, N, n)
+    rows = np.ascontiguousarray(A[ii, :])
+    cols = np.ascontiguousarray(B[:, jj])
+    # oracle: sequential k loop per output, float32
+    want = np.array([O.matmul(rows[k:k + 1], cols[:, k:k + 1])[0, 0] for k in range(n)],
+                    dtype=np.float32)
+    scale = np.array([np.abs(rows[k]).astype(np.float64) @ np.abs(cols[:, k]).astype(np.float64)
+                      for k in range(n)])
+    assert_rel(got[ii, jj], want, 1e-4, what, scale=scale)
+
+
+@pytest.mark.parametrize("M,K_,N", [(4096, 4096, 4096), (8192, 1024, 4096)])
+def test_config4_full_size(gpu, M, K_, N):
+    """Forward, dA = dG.B^T and dB = A^T.dG at the config shapes, through
+    autograd (MatmulOp), with A also given as a transposed view."""
+    r = rng(seed_of("c4", M, K_, N))
+    A = r.standard_normal((M, K_)).astype(np.float32)
+    B = (r.standard_normal((K_, N)) / np.sqrt(K_)).astype(np.float32)
+    G = r.standard_normal((M, N)).astype(np.float32)
+    for a_layout in ("contig", "transposed"):
+        xa = dev(A) if a_layout == "contig" else dev_T(A)
+        xa = xa.to("cuda")
+        xa.enable_grad()
+        xb = dev(B, requires_grad=True)
+        y = xa @ xb
+        _sampled_check(host(y), A, B, r, f"fwd {a_layout}")
+        # backward with upstream G: loss = sum(y * G) has dL/dy = G
+        loss = (y * dev(G)).sum()
+        loss.backward()
+        _sampled_check(host(xa.grad), G, np.ascontiguousarray(B.T), r, f"dA {a_layout}")
+        _sampled_check(host(xb.grad), np.ascontiguousarray(A.T), G, r, f"dB {a_layout}")

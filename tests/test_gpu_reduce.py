@@ -1,0 +1,193 @@
+"""Reductions on the GPU against the oracle (reference CPU loops).
+
+Bar: max/min values, argmax/argmin indices, tie counts and the max/min
+backward routing are bit-exact; sums/means satisfy
+|gpu - ref| <= 1e-5 * sum|x| per output (the reference sums sequentially in
+fp32, the GPU in a tree; both are within that bound of the exact sum).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import assert_bitexact, assert_rel, dev, dev_T, host, rng, seed_of
+
+import nanotorch_amd as nt
+from nanotorch_amd import _kernels as K
+from nanotorch_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+SHAPES_AXES = [
+    ((6,), (0,)),
+    ((1,), (0,)),
+    ((3, 5), (0,)),
+    ((3, 5), (1,)),
+    ((3, 5), (0, 1)),
+    ((3, 5), (1, 0)),
+    ((257, 1000), (1,)),
+    ((1000, 257), (0,)),
+    ((64, 4096), (1,)),
+    ((4096, 64), (0,)),
+    ((10, 2, 5, 1), (1, 3)),
+    ((10, 2, 5, 1), (3, 1)),
+    ((7, 9, 11), (0, 2)),
+    ((7, 9, 11), (2,)),
+    ((5, 300, 7), (1,)),
+    ((100003,), (0,)),
+]
+
+VIEWS = ["contig", "transposed", "strided"]
+
+
+def _view(a, kind):
+    if kind == "contig" or a.ndim < 2:
+        return dev(a), a
+    if kind == "transposed":
+        t = dev(np.ascontiguousarray(np.swapaxes(a, 0, -1)))
+        return t.transpose(0, a.ndim - 1), a
+    big = np.repeat(a, 2, axis=-1)
+    return dev(big)[..., ::2], big[..., ::2]
+
+
+def _sum_bound(a, axes):
+    return O.reduce(O.R_SUM, np.abs(a).astype(np.float64), axes, np.float64)
+
+
+@pytest.mark.parametrize("view", VIEWS)
+@pytest.mark.parametrize("shape,axes", SHAPES_AXES)
+def test_reduce_forward(gpu, shape, axes, view):
+    r = rng(seed_of(shape, axes, view))
+    a = r.standard_normal(shape).astype(np.float32)
+    x, a_view = _view(a, view)
+    kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+    # sum
+    got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, axes, nt.float32), kshape))
+    want = O.reduce(O.R_SUM, a_view, axes, np.float32)
+    assert_rel(got, want, 1e-5, "sum", scale=_sum_bound(a_view, axes))
+    # max / min with idx + count
+    for op, oop, aop in ((_lib.R_MAX, O.R_MAX, O.R_ARGMAX), (_lib.R_MIN, O.R_MIN, O.R_ARGMIN)):
+        v, idx, cnt = K.reduce(op, x, axes, nt.float32, want_aux=True)
+        assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), O.reduce(oop, a_view, axes), "max/min")
+        assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(aop, a_view, axes), "idx")
+    for op, oop in ((_lib.R_ARGMAX, O.R_ARGMAX), (_lib.R_ARGMIN, O.R_ARGMIN)):
+        got = host(nt.Tensor._new_contiguous(K.reduce(op, x, axes, nt.int64), kshape))
+        assert_bitexact(got, O.reduce(oop, a_view, axes), "argmax/argmin")
+
+
+def test_ties_first_index_and_count(gpu):
+    a = np.array([0.0, -1.5, -1.5, 8, 8, 3], dtype=np.float32)
+    v, idx, cnt = K.reduce(_lib.R_MAX, dev(a), (0,), nt.float32, want_aux=True)
+    assert host(nt.Tensor._new_contiguous(idx, ())) == 3
+    assert host(nt.Tensor._new_contiguous(cnt, ())) == 2
+    v, idx, cnt = K.reduce(_lib.R_MIN, dev(a), (0,), nt.float32, want_aux=True)
+    assert host(nt.Tensor._new_contiguous(idx, ())) == 1
+    # many ties spread over workgroups and segments
+    r = rng(1)
+    b = r.integers(0, 4, (64, 100000)).astype(np.float32)
+    for axes in ((1,), (0,)):
+        kshape = (64,) if axes == (1,) else (100000,)
+        _, idx, cnt = K.reduce(_lib.R_MAX, dev(b), axes, nt.float32, want_aux=True)
+        assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(O.R_ARGMAX, b, axes), "tie idx")
+        m = b.max(axis=axes[0], keepdims=True)
+        want_cnt = (b == m).sum(axis=axes[0]).astype(np.int32)
+        assert_bitexact(host(nt.Tensor._new_contiguous(cnt, kshape)), want_cnt, "tie count")
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.int32, np.int64, np.bool_])
+def test_reduce_other_dtypes(gpu, dtype):
+    r = rng(2)
+    a = (r.standard_normal((37, 53)) * 100).astype(dtype) if dtype != np.bool_ else (
+        r.integers(0, 2, (37, 53)).astype(bool))
+    for axes in ((0,), (1,), (0, 1)):
+        kshape = tuple(s for i, s in enumerate(a.shape) if i not in axes)
+        out_dt = np.int64 if dtype in (np.int32, np.int64, np.bool_) else dtype
+        got = host(nt.Tensor._new_contiguous(
+            K.reduce(_lib.R_SUM, dev(a), axes, nt.Tensor(np.zeros(1, out_dt)).dtype), kshape))
+        want = O.reduce(O.R_SUM, a, axes, out_dt)
+        if dtype == np.float64:
+            assert_rel(got, want, 1e-12, "f64 sum", scale=_sum_bound(a, axes))
+        else:
+            assert_bitexact(got, want, "int sum")
+        for op, oop in ((_lib.R_MAX, O.R_MAX), (_lib.R_MIN, O.R_MIN), (_lib.R_ARGMAX, O.R_ARGMAX)):
+            odt = nt.int64 if op == _lib.R_ARGMAX else dev(a).dtype
+            got = host(nt.Tensor._new_contiguous(K.reduce(op, dev(a), axes, odt), kshape))
+            assert_bitexact(got, O.reduce(oop, a, axes), f"{dtype} op {op}")
+
+
+def test_sum_into_wider_dtype(gpu):
+    a = rng(3).standard_normal((300, 500)).astype(np.float32)
+    got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, dev(a), (1,), nt.float64), (300,)))
+    want = O.reduce(O.R_SUM, a, (1,), np.float64)
+    assert_rel(got, want, 1e-12, "f32->f64 sum", scale=_sum_bound(a, (1,)))
+
+
+# --------------------------------------------------------------- backward
+
+
+@pytest.mark.parametrize("acc", [False, True])
+@pytest.mark.parametrize("shape,axes", [((300, 200), (0,)), ((300, 200), (1,)),
+                                        ((300, 200), (0, 1)), ((4, 6, 8), (2, 0))])
+@pytest.mark.parametrize("op", ["max", "min"])
+def test_select_backward(gpu, op, shape, axes, acc):
+    r = rng(seed_of(op, shape, axes, acc))
+    a = r.integers(-20, 20, shape).astype(np.float32)  # plenty of ties
+    a[0] = r.standard_normal(shape[1:]) if len(shape) > 1 else a[0]
+    kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+    g = r.standard_normal(kshape).astype(np.float32)
+    nop = _lib.R_MAX if op == "max" else _lib.R_MIN
+    oop = O.R_MAX if op == "max" else O.R_MIN
+    _, idx, cnt = K.reduce(nop, dev(a), axes, nt.float32, want_aux=True)
+    want = O.sel_bwd(oop, g, a, axes)
+    old = r.standard_normal(shape).astype(np.float32)
+    if acc:
+        tgt = dev(old)
+        K.reduce_bwd(nop, dev(g), 1.0, idx, cnt, axes, shape, tgt)
+        got = host(tgt)
+        want = O.accumulate(old, want)
+    else:
+        st = K.reduce_bwd(nop, dev(g), 1.0, idx, cnt, axes, shape, None)
+        got = host(nt.Tensor._new_contiguous(st, shape))
+    assert_bitexact(got, want, f"{op} bwd")
+
+
+@pytest.mark.parametrize("acc", [False, True])
+def test_mean_backward(gpu, acc):
+    r = rng(5)
+    shape, axes = (123, 77), (1,)
+    g = r.standard_normal((123,)).astype(np.float32)
+    n = 77
+    # ops_reduction.py:129-138: expand(g) / denom
+    want = O.binary(O.DIV, np.broadcast_to(g.reshape(123, 1), shape),
+                    np.broadcast_to(O.scalar(n, np.float32), shape))
+    old = r.standard_normal(shape).astype(np.float32)
+    if acc:
+        tgt = dev_T(old)
+        K.reduce_bwd(_lib.R_MEAN, dev(g), float(n), None, None, axes, shape, tgt)
+        assert_bitexact(host(tgt), O.accumulate(old, want), "mean bwd acc")
+    else:
+        st = K.reduce_bwd(_lib.R_MEAN, dev(g), float(n), None, None, axes, shape, None)
+        assert_bitexact(host(nt.Tensor._new_contiguous(st, shape)), want, "mean bwd")
+
+
+@pytest.mark.parametrize("axes", [(0,), (1,), (0, 1)])
+def test_config3_full_size(gpu, axes):
+    """[8192, 8192] fp32: sum within the condition-aware bound, max value /
+    index bit-exact, max backward routing bit-exact."""
+    r = rng(seed_of("c3", axes))
+    shape = (8192, 8192)
+    a = r.standard_normal(shape).astype(np.float32)
+    x = dev(a)
+    kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+    got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, axes, nt.float32), kshape))
+    want = O.reduce(O.R_SUM, a, axes, np.float32)
+    assert_rel(got, want, 1e-5, "sum 2^26", scale=_sum_bound(a, axes))
+    v, idx, cnt = K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True)
+    assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), O.reduce(O.R_MAX, a, axes), "max 2^26")
+    assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(O.R_ARGMAX, a, axes), "argmax 2^26")
+    if axes != (0, 1):
+        g = r.standard_normal(kshape).astype(np.float32)
+        st = K.reduce_bwd(_lib.R_MAX, dev(g), 1.0, idx, cnt, axes, shape, None)
+        assert_bitexact(host(nt.Tensor._new_contiguous(st, shape)), O.sel_bwd(O.R_MAX, g, a, axes), "max bwd 2^26")
