@@ -20,8 +20,11 @@
 //   mul      (b * g, a * g)                       ops_binary.py:145-150
 //   div      (g / b, ((-a) / pow(b, 2)) * g)      ops_binary.py:197-202
 //
-// pow(v, -1) and pow(v, 2) are evaluated as 1 / v and v * v: both are what a
-// correctly rounded pow returns, and glibc's powf returns them bit for bit.
+// pow(v, -1) and pow(v, 2) are evaluated as 1 / v and v * v, the correctly
+// rounded values.  The reference calls the host powf there; glibc's powf
+// is one ulp off correct rounding for a fraction of a percent of inputs, so
+// those chains (log, sqrt, tanh, the b-gradient of div) agree with the
+// reference to within that ulp; the others are bit-identical.
 // pow(x, e - 1) for a general e stays a pow call; e - 1 is formed in fp32
 // as the reference does with its fp32 exponent tensor.  Accumulate mode is
 // `old + term` with one rounding, the reference's add_inplace

@@ -1,10 +1,18 @@
 """Elementwise family on the GPU against the oracle (reference CPU loops).
 
-Bar: bit-exact for +, -, *, /, neg, relu, sqrt, comparisons, casts and for
-the fused backward chains given the same saved tensors (their only non-IEEE
-step, pow(v, 2) / pow(v, -1), equals v*v / 1/v in glibc, checked on the CPU
-in test_oracle_pinning.py); rel 1e-6 for exp/log/tanh/sigmoid/pow forward
-and the pow backward (device libm vs host libm, a few ulps).
+Bar:
+  * bit-exact: +, -, *, /, neg, relu, sqrt forward, comparisons, casts, and
+    the fused backward chains made of IEEE ops only (neg, exp, sigmoid,
+    relu, add, sub, mul, the a-gradient of div), given the same saved
+    tensors;
+  * rel 1e-6: exp/log/tanh/sigmoid/pow forward (device vs host libm);
+  * rel 1e-6 against a condition-aware scale: chains whose reference form
+    calls powf (log: x**-1, sqrt: y**-1, tanh: y**2, div b-gradient: b**2,
+    pow: x**(e-1)).  glibc's powf is off correct rounding by one ulp on a
+    fraction of a percent of inputs (test_oracle_pinning.py), the GPU
+    evaluates v*v and 1/v correctly rounded, so the chains can differ by
+    that ulp times the chain's sensitivity: |g|*(1 + y*y) for tanh,
+    |result| otherwise, plus |old| in accumulate mode.
 """
 
 from __future__ import annotations
@@ -221,9 +229,13 @@ def test_unary_backward_kernel(gpu, name, op, oop, chain, dom, saved, layout, ac
     e = 2.5 if name == "pow" else 0.0
     s = None if saved == "none" else (x if saved == "in" else O.unary(oop, x, e))
     want = chain(g, s)
+    scale = np.abs(want).astype(np.float64)
+    if name == "tanh":
+        scale = np.abs(g).astype(np.float64) * (1 + s.astype(np.float64) ** 2)
     old = r.standard_normal(shape).astype(np.float32)
     if acc:
         want = O.accumulate(old, want)
+        scale = scale + np.abs(old)
     sv = None if s is None else _mk(s, layout)
     if acc:
         tgt = _mk(old, layout)
@@ -232,8 +244,8 @@ def test_unary_backward_kernel(gpu, name, op, oop, chain, dom, saved, layout, ac
     else:
         st = K.unary_bwd(op, dev(g), sv, e, None)
         got = host(nt.Tensor._new_contiguous(st, shape))
-    if name == "pow":
-        assert_rel(got, want, 1e-6, name)
+    if name in ("pow", "log", "sqrt", "tanh"):
+        assert_rel(got, want, 1e-6, name, scale=scale)
     else:
         assert_bitexact(got, want, name)
 
@@ -254,12 +266,17 @@ def test_binary_backward_kernel(gpu, name, op, oop, need, acc):
     for i, (n, s_, w) in enumerate(((need[0], sa, ga_w), (need[1], sb, gb_w))):
         if not n:
             continue
+        scale = np.abs(w).astype(np.float64)
         if acc[i]:
             got = host(tg[i])
             w = O.accumulate(olds[i], w)
+            scale = scale + np.abs(olds[i])
         else:
             got = host(nt.Tensor._new_contiguous(s_, shape))
-        assert_bitexact(got, w, f"{name} grad {i}")
+        if name == "div" and i == 1:  # reference form: (-a) / b**2 * g
+            assert_rel(got, w, 1e-6, f"{name} grad {i}", scale=scale)
+        else:
+            assert_bitexact(got, w, f"{name} grad {i}")
 
 
 # ------------------------------------------------------------ config 2 size

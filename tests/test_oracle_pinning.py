@@ -1,0 +1,388 @@
+"""Pins the oracle (CPU restatement of the reference) before it is trusted.
+
+Checks, all on the CPU:
+  * the reference test-suite's known-answer tables (tests/golden/
+    known_answers.json, transcribed by tests/golden/make_golden.py);
+  * mathematics: math-module values, fp64 exact sums, fp64 products,
+    analytic derivatives and central differences of every backward chain,
+    one-hot routing of max/min backward, brute-force small cases;
+  * the libm identities the GPU kernels rely on (powf(v,2) == v*v,
+    powf(v,-1) == 1/v bit for bit);
+  * planted mistakes in the oracle (wrong operand, dropped term) are caught.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KA = json.load(open(os.path.join(HERE, "golden", "known_answers.json")))
+
+
+def _np_of(v, dtype=None):
+    """numpy array as the reference's Tensor(v) would hold it: bool / int64 /
+    float32 inferred from the Python values (core.py:573-636)."""
+    if dtype is not None:
+        return np.array(v, dtype=dtype)
+    flat = np.array(v, dtype=object).ravel().tolist() if isinstance(v, list) else [v]
+    if any(isinstance(x, float) for x in flat):
+        return np.array(v, dtype=np.float32)
+    if all(isinstance(x, bool) for x in flat) and flat:
+        return np.array(v, dtype=np.bool_)
+    return np.array(v, dtype=np.int64)
+
+
+def _promote(*arrs):
+    code = max(O._CODES[a.dtype] for a in arrs)
+    return [O.cast(a, O._NP[code]) for a in arrs]
+
+
+# ------------------------------------------------------- known answers
+
+
+@pytest.mark.parametrize("case", KA["unary"], ids=lambda c: f"{c['op']}-{c['input']}")
+def test_unary_known_answers(case):
+    x = _np_of(case["input"])
+    if case["op"] == "pow":
+        e = case["exponent"]
+        et = _np_of(e)
+        (x2,) = _promote(x, et)[:1]
+        got = O.unary(O.POW, np.ascontiguousarray(x2), float(et))
+    else:
+        if case["op"] != "relu":
+            x = O.cast(x, np.float32) if x.dtype != np.float32 else x
+        op = {"exp": O.EXP, "log": O.LOG, "relu": O.RELU}[case["op"]]
+        got = O.unary(op, np.ascontiguousarray(x))
+    want = np.array(case["expected"], dtype=np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= case["tol"] + 1e-7 * np.abs(want)), (
+        case, got)
+
+
+@pytest.mark.parametrize("case", KA["binary"], ids=lambda c: f"{c['op']}-{c['src'][-7:]}")
+def test_binary_known_answers(case):
+    a, b = _np_of(case["a"]), _np_of(case["b"])
+    a, b = _promote(a, b)
+    shape = np.broadcast_shapes(a.shape, b.shape)
+    a, b = np.broadcast_to(a, shape), np.broadcast_to(b, shape)
+    op = case["op"]
+    if op in ("lt", "le"):  # x < y is y > x (__init__.py:172-173)
+        a, b, op = b, a, {"lt": "gt", "le": "ge"}[op]
+    code = {"add": O.ADD, "sub": O.SUB, "mul": O.MUL, "div": O.DIV,
+            "eq": O.EQ, "gt": O.GT, "ge": O.GE}[op]
+    got = O.binary(code, a, b)
+    want = _np_of(case["expected"])
+    if got.dtype != np.bool_:
+        want = want.astype(got.dtype)
+    assert np.array_equal(got, np.broadcast_to(want, got.shape)), (case, got)
+
+
+def test_matmul_known_answers():
+    a23 = np.array(KA["matmul_a23"], dtype=np.float32)
+    ar12 = np.arange(12, dtype=np.float32).reshape(3, 4)
+    named = {"a23.T": a23.T, "arange12[:, ::2]": ar12[:, ::2]}
+    for case in KA["matmul"]:
+        a = named.get(case["a"]) if isinstance(case["a"], str) else np.array(case["a"], np.float32)
+        b = named.get(case["b"]) if isinstance(case["b"], str) else np.array(case["b"], np.float32)
+        if a.ndim == 1:  # (k,) @ (k,) -> () through (1,k) @ (k,1)
+            got = O.matmul(a.reshape(1, -1), b.reshape(-1, 1))[0, 0]
+        else:
+            got = O.matmul(a, b)
+        assert np.array_equal(got, np.array(case["expected"], np.float32)), case
+
+
+@pytest.mark.parametrize("case", KA["reduction"], ids=lambda c: c["op"])
+def test_reduction_known_answers(case):
+    op = case["op"]
+    if op == "sum":
+        x = _np_of(case["input"])
+        axis = case["axis"]
+        axes = tuple(range(x.ndim)) if axis is None else (
+            (axis,) if isinstance(axis, int) else tuple(axis))
+        axes = tuple(a + x.ndim if a < 0 else a for a in axes)
+        out_dt = np.float32 if x.dtype == np.float32 else np.int64  # max(dtype, Int64)
+        got = O.reduce(O.R_SUM, x, axes, out_dt)
+        if case["keepdim"]:
+            got = got.reshape(case["shape"])
+        assert list(got.shape) == case["shape"]
+        assert got.tolist() == case["expected"]
+    elif op == "select":
+        x = np.array(case["input"], dtype=np.float32)
+        assert O.reduce(O.R_MAX, x, (0,)) == case["max"]
+        assert O.reduce(O.R_ARGMAX, x, (0,)) == case["argmax"]
+        assert O.reduce(O.R_MIN, x, (0,)) == case["min"]
+        assert O.reduce(O.R_ARGMIN, x, (0,)) == case["argmin"]
+    elif op == "sum_default_dtype":
+        x = np.array(case["input"], dtype=case["dtype"])
+        out_dt = np.dtype(case["out_dtype"])
+        assert O.reduce(O.R_SUM, x, (0,), out_dt).dtype == out_dt
+    elif op == "sum_dtype_kwarg":
+        x = np.array(case["input"], dtype=case["dtype"])
+        got = O.reduce(O.R_SUM, x, (0,), np.dtype(case["kwarg"]))
+        assert got.tolist() == case["expected"]
+    elif op == "mean_dtype_kwarg":
+        x = np.array(case["input"], dtype=case["dtype"])
+        s = O.reduce(O.R_SUM, x, (0,), np.dtype(case["kwarg"]))
+        got = O.binary(O.DIV, s, O.scalar(3, s.dtype))
+        assert got.tolist() == case["expected"]
+
+
+def _autograd_case(case):
+    f = np.float32
+    one = np.array(1.0, dtype=f)
+    c = case["case"]
+    if c == "3x":
+        # loss = 3 * x: MulOp(x, Tensor(3)) -> grad_x = x2 * g
+        return [O.binary(O.MUL, O.scalar(3, f), one)]
+    if c == "exp(3x)":
+        x = np.array(case["x"], f)
+        y = O.binary(O.MUL, x, O.scalar(3, f))
+        ey = O.unary(O.EXP, y)
+        gy = O.bwd_exp(one, ey)
+        return [O.binary(O.MUL, O.scalar(3, f), gy)]
+    if c in ("log(x1*x2)", "sum(log(x1*x2))"):
+        x1, x2 = np.array(case["x1"], f), np.array(case["x2"], f)
+        y = O.binary(O.MUL, x1, x2)
+        g = np.broadcast_to(one, y.shape).copy()
+        gy = O.bwd_log(g, y)
+        return O.bwd_binary(O.MUL, gy, x1, x2)
+    if c == "sum(sum(x,0))":
+        x = np.array(case["x"], f)
+        return [np.broadcast_to(one, x.shape)]
+    if c == "sum(x.T*g)":
+        g = np.array(case["g"], np.int64)
+        gf = O.cast(g, f)  # MulOp promotes the int64 g to float32
+        return [np.ascontiguousarray(O.binary(O.MUL, gf, np.ones_like(gf)).T)]
+    if c == "sum(2*exp(x)+3*exp(x))":
+        x = np.array(case["x"], f)
+        a = O.unary(O.EXP, x)
+        g = np.ones(2, f)
+        gb = O.binary(O.MUL, O.cast(np.full(2, 2, np.int64), f), g)
+        gc = O.binary(O.MUL, O.cast(np.full(2, 3, np.int64), f), g)
+        ga = O.accumulate(gb, gc)
+        return [O.bwd_exp(ga, a)]
+    raise KeyError(c)
+
+
+@pytest.mark.parametrize("case", KA["autograd"], ids=lambda c: c["case"])
+def test_autograd_known_answers(case):
+    got = _autograd_case(case)
+    wants = [case[k] for k in ("grad", "g1", "g2") if k in case]
+    for g, w in zip(got, wants):
+        w = np.array(w, dtype=np.float64)
+        assert np.all(np.abs(g.astype(np.float64) - w) <= case["tol"] + 1e-7 * np.abs(w)), (
+            case, g)
+
+
+# ------------------------------------------------------------ mathematics
+
+
+def test_unary_vs_math_module():
+    # the reference's own check (test_tensor_unary_ops.py:145-165), tightened:
+    # fp64 libm is within 1 ulp of the math module.
+    r = np.random.default_rng(42)
+    x = r.random(50) + 0.5
+    cases = [(O.EXP, math.exp, 0.0), (O.LOG, math.log, 0.0), (O.SQRT, math.sqrt, 0.0),
+             (O.TANH, math.tanh, 0.0), (O.SIGMOID, lambda v: 1 / (1 + math.exp(-v)), 0.0),
+             (O.POW, lambda v: math.pow(v, 3.14), 3.14), (O.POW, lambda v: math.pow(v, -3.14), -3.14),
+             (O.POW, lambda v: math.pow(v, 0), 0.0)]
+    for op, fn, e in cases:
+        got = O.unary(op, x, e)
+        want = np.array([fn(v) for v in x])
+        assert np.all(np.abs(got - want) <= 4e-16 * np.abs(want)), op
+
+
+def test_sum_vs_exact():
+    r = np.random.default_rng(1)
+    x = r.standard_normal((37, 4001)).astype(np.float32)
+    got = O.reduce(O.R_SUM, x, (1,), np.float32)
+    exact = np.array([math.fsum(row.astype(np.float64)) for row in x])
+    bound = np.abs(x).astype(np.float64).sum(1) * 4001 * 2**-24  # sequential fp32 bound
+    assert np.all(np.abs(got - exact) <= bound)
+    # axis-tuple order defines the argmax index over several axes
+    y = r.standard_normal((3, 4, 5)).astype(np.float32)
+    j = O.reduce(O.R_ARGMAX, y, (2, 0))
+    for k in range(4):
+        sl = y[:, k, :].T.ravel()  # drop order (axis 2, axis 0), row-major
+        assert j[k] == int(np.argmax(sl))
+
+
+def test_matmul_vs_fp64():
+    r = np.random.default_rng(2)
+    a = r.standard_normal((33, 70)).astype(np.float32)
+    b = r.standard_normal((70, 41)).astype(np.float32)
+    got = O.matmul(a, b)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    bound = (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)) * 70 * 2**-24
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.array_equal(O.matmul(a, b, parallel=True), got)  # OpenMP: bit-identical
+    # batched with strided / broadcast operands, brute force
+    A = r.standard_normal((2, 3, 5, 4)).astype(np.float32)
+    B = r.standard_normal((4, 6)).astype(np.float32)
+    got = O.matmul(A, np.broadcast_to(B, (2, 3, 4, 6)))
+    for i in range(2):
+        for j in range(3):
+            assert np.allclose(got[i, j], A[i, j].astype(np.float64) @ B, rtol=1e-6, atol=1e-6)
+
+
+def _fd(fn, x, h=1e-6):
+    return (fn(x + h) - fn(x - h)) / (2 * h)
+
+
+@pytest.mark.parametrize("name", ["neg", "exp", "log", "sqrt", "tanh", "sigmoid", "relu", "pow"])
+def test_unary_chains_are_derivatives(name):
+    """fp64 chains equal the analytic derivative and central differences."""
+    r = np.random.default_rng(3)
+    x = r.uniform(0.2, 3.0, 200)
+    g = r.standard_normal(200)
+    f = {"neg": lambda v: -v, "exp": np.exp, "log": np.log, "sqrt": np.sqrt,
+         "tanh": np.tanh, "sigmoid": lambda v: 1 / (1 + np.exp(-v)),
+         "relu": lambda v: np.maximum(v, 0), "pow": lambda v: v**2.5}[name]
+    op = {"exp": O.EXP, "log": O.LOG, "sqrt": O.SQRT, "tanh": O.TANH, "sigmoid": O.SIGMOID,
+          "relu": O.RELU}.get(name)
+    y = O.unary(op, x) if op is not None else None
+    chain = {
+        "neg": lambda: O.bwd_neg(g), "exp": lambda: O.bwd_exp(g, y), "log": lambda: O.bwd_log(g, x),
+        "sqrt": lambda: O.bwd_sqrt(g, y), "tanh": lambda: O.bwd_tanh(g, y),
+        "sigmoid": lambda: O.bwd_sigmoid(g, y), "relu": lambda: O.bwd_relu(g, y),
+        "pow": lambda: O.bwd_pow(g, x, 2.5),
+    }[name]()
+    deriv = g * _fd(f, x)
+    assert np.allclose(chain, deriv, rtol=1e-6, atol=1e-8), name
+
+
+@pytest.mark.parametrize("name,op", [("add", O.ADD), ("sub", O.SUB), ("mul", O.MUL), ("div", O.DIV)])
+def test_binary_chains_are_derivatives(name, op):
+    r = np.random.default_rng(4)
+    a = r.uniform(0.5, 2, 100)
+    b = r.uniform(0.5, 2, 100)
+    g = r.standard_normal(100)
+    fn = {O.ADD: np.add, O.SUB: np.subtract, O.MUL: np.multiply, O.DIV: np.divide}[op]
+    ga, gb = O.bwd_binary(op, g, a, b)
+    assert np.allclose(ga, g * _fd(lambda v: fn(v, b), a), rtol=1e-6)
+    assert np.allclose(gb, g * _fd(lambda v: fn(a, v), b), rtol=1e-6)
+
+
+def test_select_backward_routing():
+    r = np.random.default_rng(5)
+    x = r.standard_normal((6, 9)).astype(np.float32)
+    x[2, 4] = x[2, 7] = 5.0  # tie in row 2
+    g = r.standard_normal(6).astype(np.float32)
+    got = O.sel_bwd(O.R_MAX, g, x, (1,))
+    for i in range(6):
+        row = np.zeros(9, np.float32)
+        if i != 2:
+            row[int(np.argmax(x[i]))] = g[i]
+        # ties route 0 (1 / count is an int64 division); zeros are g * 0.0
+        assert np.array_equal(got[i], row + g[i] * np.float32(0)), i
+    assert np.array_equal(np.signbit(got[2]), np.full(9, g[2] < 0))
+
+
+def _ulps(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    ia = a.view(np.int32).astype(np.int64)
+    ib = b.view(np.int32).astype(np.int64)
+    return np.abs(ia - ib)
+
+
+def test_glibc_pow_vs_correct_rounding():
+    """The GPU evaluates pow(v, 2) and pow(v, -1) of the backward chains as
+    v*v and 1/v (correctly rounded).  glibc's powf is not always correctly
+    rounded: it differs from those in a fraction of a percent of inputs, by
+    exactly one ulp.  That bounds the chains' GPU/oracle gap (the tolerance
+    of the log / sqrt / tanh / div-b backward parity tests)."""
+    r = np.random.default_rng(6)
+    v = r.uniform(-8, 8, 1_000_000).astype(np.float32)
+    v = v[v != 0]
+    p2 = O.unary(O.POW, v, 2.0)
+    d2 = _ulps(p2, v * v)
+    assert d2.max() <= 1 and 0 < (d2 > 0).mean() < 0.01
+    av = np.abs(v)
+    pm = O.unary(O.POW, av, -1.0)
+    dm = _ulps(pm, np.float32(1) / av)
+    assert dm.max() <= 1 and 0 < (dm > 0).mean() < 0.01
+    # exponent 1 (the MSE backward's pow(d, 2 - 1)) is exact
+    assert np.array_equal(O.unary(O.POW, v, 1.0), v)
+
+
+def test_mlp_step_gradients_vs_fp64():
+    """The oracle's MLP step updates the weights by -lr * dL/dW, checked
+    against an fp64 re-derivation of the same network."""
+    r = np.random.default_rng(7)
+    x = r.standard_normal((16, 12)).astype(np.float32)
+    t = r.standard_normal((16, 5)).astype(np.float32)
+    dims = [12, 10, 8, 5]
+    params = [((r.standard_normal((dims[i], dims[i + 1])) * 0.5).astype(np.float32),
+               (r.standard_normal(dims[i + 1]) * 0.1).astype(np.float32)) for i in range(3)]
+    acts = ["tanh", "sigmoid"]
+    before = [(W.copy(), b.copy()) for W, b in params]
+    lr = 0.5
+    loss = O.mlp_step(params, x, t, acts, lr)
+    # fp64 reference derivation
+    P = [(W.astype(np.float64), b.astype(np.float64)) for W, b in before]
+    h = [x.astype(np.float64)]
+    z1 = h[0] @ P[0][0] + P[0][1]
+    a1 = np.tanh(z1)
+    z2 = a1 @ P[1][0] + P[1][1]
+    a2 = 1 / (1 + np.exp(-z2))
+    y = a2 @ P[2][0] + P[2][1]
+    d = y - t
+    L = (d**2).mean()
+    assert abs(float(loss) - L) <= 1e-5 * L
+    gy = 2 * d / d.size
+    gW3, gb3 = a2.T @ gy, gy.sum(0)
+    g2 = (gy @ P[2][0].T) * a2 * (1 - a2)
+    gW2, gb2 = a1.T @ g2, g2.sum(0)
+    g1 = (g2 @ P[1][0].T) * (1 - a1**2)
+    gW1, gb1 = h[0].T @ g1, g1.sum(0)
+    for (W, b), (W0, b0), gW, gb in zip(params, before, (gW1, gW2, gW3), (gb1, gb2, gb3)):
+        assert np.allclose((W0.astype(np.float64) - W) / lr, gW, rtol=1e-3, atol=1e-6)
+        assert np.allclose((b0.astype(np.float64) - b) / lr, gb, rtol=1e-3, atol=1e-6)
+
+
+# ------------------------------------------------------- planted mistakes
+
+
+def test_planted_mistakes_are_caught(monkeypatch):
+    """A swapped operand or a dropped term in the oracle fails the pins."""
+    good = O.bwd_binary
+
+    def swapped(op, g, a, b):
+        ga, gb = good(op, g, a, b)
+        return (gb, ga) if op == O.DIV else (ga, gb)
+
+    monkeypatch.setattr(O, "bwd_binary", swapped)
+    with pytest.raises(AssertionError):
+        test_binary_chains_are_derivatives("div", O.DIV)
+    monkeypatch.setattr(O, "bwd_binary", good)
+
+    good_tanh = O.bwd_tanh
+    monkeypatch.setattr(O, "bwd_tanh", lambda g, y: O.binary(O.MUL, g, O.rsub_scalar(1, y)))
+    with pytest.raises(AssertionError):
+        test_unary_chains_are_derivatives("tanh")
+    monkeypatch.setattr(O, "bwd_tanh", good_tanh)
+
+    good_pow = O.bwd_pow
+    monkeypatch.setattr(O, "bwd_pow", lambda g, x, e: O.binary(O.MUL, g, O.pow_scalar(x, e - 1)))
+    with pytest.raises(AssertionError):
+        test_unary_chains_are_derivatives("pow")
+    monkeypatch.setattr(O, "bwd_pow", good_pow)
+
+
+def test_rng_known_answer():
+    import ctypes
+
+    from nanotorch_amd import _lib
+
+    lib = _lib.load()
+    buf = (ctypes.c_float * 2)()
+    lib.nt_manual_seed(KA["rng"]["seed"])
+    lib.nt_host_uniform(ctypes.addressof(buf), 3, 2, 0.0, 1.0)
+    assert buf[0] == np.float32(KA["rng"]["first"])
+    # MSVC's value differs by one ulp (libstdc++ vs MSVC STL)
+    assert abs(buf[1] - KA["rng"]["second_msvc"]) <= 2 * np.spacing(np.float32(0.64))
