@@ -1,0 +1,446 @@
+"""Benchmark of the MI355X hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--parts all|none|...]
+
+Headline (`value`): config 2 of BASELINE.json -- the elementwise forward +
+fused backward sweep at 2^24 fp32 elements ([4096, 4096]): each of add, sub,
+mul, truediv, neg, exp, log, sqrt, pow(2.5), relu, sigmoid, tanh, forward then
+backward in accumulate mode, once on contiguous tensors and once on
+transposed (`.T`) views.  One step = one full sweep (48 kernels).  `value` is
+the sweep's algorithmic HBM bytes / its time (GB/s); inputs are resident in
+HBM before timing.  Timing uses HIP events on the library stream.
+
+Parts reported beside it: config 3 reductions (GB/s), config 4 MatMulOp
+forward + dA + dB (TFLOP/s), config 5 4-layer MLP training steps (step/s and
+the loss trace), plus a single-threaded CPU baseline (the oracle, i.e. the
+reference's CPU kernels restated) on a bounded sample of the headline
+workload.
+
+Data is synthetic (seeded normal / uniform per config); weights of the MLP
+are random He-normal.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import nanotorch_amd as nt  # noqa: E402
+from nanotorch_amd import _kernels as K  # noqa: E402
+from nanotorch_amd import _lib  # noqa: E402
+from nanotorch_amd import nn  # noqa: E402
+from nanotorch_amd._storage import Storage  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
+
+BASELINE_METRIC = "matmul fwd+bwd fp32 TFLOP/s; elementwise/reduce HBM GB/s; MLP step/s"
+
+
+# ----------------------------------------------------------------- helpers
+
+
+def dev(a: np.ndarray) -> nt.Tensor:
+    return nt.Tensor(np.ascontiguousarray(a), device="cuda")
+
+
+def dev_T(a: np.ndarray) -> nt.Tensor:
+    return dev(np.ascontiguousarray(a.T)).T
+
+
+def view(t) -> _lib.NtView:
+    return K.view_of(t)
+
+
+class Timer:
+    """Brackets launches with HIP events on the library stream."""
+
+    def __init__(self) -> None:
+        self.marks: list[tuple[str, _lib.Event, _lib.Event]] = []
+
+    def run(self, name: str, fn) -> None:
+        a, b = _lib.Event(), _lib.Event()
+        a.record()
+        fn()
+        b.record()
+        self.marks.append((name, a, b))
+
+    def durations(self) -> dict[str, list[float]]:
+        out: dict[str, list[float]] = {}
+        for name, a, b in self.marks:
+            out.setdefault(name, []).append(a.elapsed_ms(b))
+        return out
+
+
+def _fresh(shape, dtype=nt.float32) -> nt.Tensor:
+    return nt.Tensor._new_contiguous(Storage.allocate(math.prod(shape), dtype, nt.Device.Cuda), shape)
+
+
+# --------------------------------------------------- config 2: elementwise
+
+UNARY_OPS = [  # name, op, domain, saved ("in" | "out" | None), exponent
+    ("neg", _lib.NEG, (-4, 4), None, 0.0),
+    ("exp", _lib.EXP, (-4, 4), "out", 0.0),
+    ("log", _lib.LOG, (0.1, 4), "in", 0.0),
+    ("sqrt", _lib.SQRT, (0.1, 4), "out", 0.0),
+    ("pow", _lib.POW, (0.1, 4), "in", 2.5),
+    ("relu", _lib.RELU, None, "out", 0.0),
+    ("sigmoid", _lib.SIGMOID, None, "out", 0.0),
+    ("tanh", _lib.TANH, None, "out", 0.0),
+]
+BINARY_OPS = [("add", _lib.ADD), ("sub", _lib.SUB), ("mul", _lib.MUL), ("truediv", _lib.DIV)]
+
+N_ELEM = 4096 * 4096
+
+
+def ew_bytes(name: str, phase: str) -> int:
+    """Algorithmic bytes per launch (fp32, 2^24 elements): each distinct
+    tensor read once, each output written once.  Backward is accumulate
+    mode: reads g (+ saved inputs) + old grads, writes the grads."""
+    per = {
+        ("fwd", "bin"): 12, ("fwd", "un"): 8,
+        ("bwd", "add"): 20, ("bwd", "sub"): 20, ("bwd", "mul"): 28, ("bwd", "truediv"): 28,
+        ("bwd", "neg"): 12,
+    }
+    binary = name in ("add", "sub", "mul", "truediv")
+    if phase == "fwd":
+        return per[("fwd", "bin" if binary else "un")] * N_ELEM
+    return per.get(("bwd", name), 16) * N_ELEM
+
+
+class ElementwiseSweep:
+    """Prepared tensors and C views for the config-2 sweep; `step()` queues
+    the 48 kernels through the C ABI with no allocation in the loop."""
+
+    def __init__(self, seed: int = 0) -> None:
+        r = np.random.default_rng(seed)
+        shape = (4096, 4096)
+        self.calls: list[tuple[str, str, str, object]] = []  # (op, layout, phase, fn)
+        lib = _lib.load()
+        keep = []  # keep tensors alive
+        for layout in ("contig", "transposed"):
+            mk = dev if layout == "contig" else dev_T
+            for name, op in BINARY_OPS:
+                a = r.standard_normal(shape).astype(np.float32)
+                b = (r.uniform(0.5, 2, shape) if name == "truediv" else r.standard_normal(shape)).astype(np.float32)
+                g = r.standard_normal(shape).astype(np.float32)
+                ta, tb, tg = mk(a), mk(b), dev(g)
+                out = _fresh(shape)
+                # accumulation targets laid out like the inputs
+                ga, gb = mk(r.standard_normal(shape).astype(np.float32)), mk(r.standard_normal(shape).astype(np.float32))
+                va, vb, vg, vo, vga, vgb = view(ta), view(tb), view(tg), view(out), view(ga), view(gb)
+                keep += [ta, tb, tg, out, ga, gb, va, vb, vg, vo, vga, vgb]
+                self.calls.append((name, layout, "fwd", (lib.nt_binary, (op, ctypes.byref(va), ctypes.byref(vb), ctypes.byref(vo)))))
+                self.calls.append((name, layout, "bwd", (lib.nt_binary_bwd, (
+                    op, ctypes.byref(vg), ctypes.byref(va), ctypes.byref(vb),
+                    ctypes.byref(vga), 1, ctypes.byref(vgb), 1))))
+            for name, op, dom, saved, e in UNARY_OPS:
+                x = (r.standard_normal(shape) if dom is None else r.uniform(dom[0], dom[1], shape)).astype(np.float32)
+                g = r.standard_normal(shape).astype(np.float32)
+                tx, tg = mk(x), dev(g)
+                out = _fresh(shape)
+                gx = mk(r.standard_normal(shape).astype(np.float32))
+                vx, vg, vo, vgx = view(tx), view(tg), view(out), view(gx)
+                # saved tensor: the forward output (contiguous) or the input view
+                vs = vo if saved == "out" else (vx if saved == "in" else None)
+                keep += [tx, tg, out, gx, vx, vg, vo, vgx]
+                self.calls.append((name, layout, "fwd", (lib.nt_unary, (op, ctypes.byref(vx), e, ctypes.byref(vo)))))
+                self.calls.append((name, layout, "bwd", (lib.nt_unary_bwd, (
+                    op, ctypes.byref(vg), ctypes.byref(vs) if vs is not None else None, e,
+                    ctypes.byref(vgx), 1))))
+        self._keep = keep
+        self.step_bytes = sum(ew_bytes(n, ph) for n, _, ph, _ in self.calls)
+
+    def step(self, timer: Timer | None = None) -> None:
+        for name, layout, phase, (fn, args) in self.calls:
+            if timer is None:
+                _lib.check(fn(*args))
+            else:
+                timer.run(f"{name}|{layout}|{phase}", lambda fn=fn, args=args: _lib.check(fn(*args)))
+
+
+def bench_elementwise(steps: int, warmup: int) -> dict:
+    sw = ElementwiseSweep()
+    for _ in range(warmup):
+        sw.step()
+    nt.sync()
+    # whole-step timing: events around the K steps only
+    t0, t1 = _lib.Event(), _lib.Event()
+    nt.sync()
+    t0.record()
+    for _ in range(steps):
+        sw.step()
+    t1.record()
+    nt.sync()
+    total_ms = t0.elapsed_ms(t1)
+    # per-kernel timing (separate pass, events around each launch)
+    tm = Timer()
+    for _ in range(max(2, steps // 2)):
+        sw.step(tm)
+    nt.sync()
+    per = {}
+    for key, ds in tm.durations().items():
+        name, layout, phase = key.split("|")
+        avg = sum(ds) / len(ds)
+        gbs = ew_bytes(name, phase) / (avg * 1e-3) / 1e9
+        per[key] = {"ms": round(avg, 5), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "bytes": ew_bytes(name, phase)}
+    return {"ms_per_step": total_ms / steps, "step_bytes": sw.step_bytes, "per_kernel": per}
+
+
+# ---------------------------------------------------- config 3: reductions
+
+
+def bench_reductions(iters: int = 5) -> dict:
+    r = np.random.default_rng(3)
+    shape = (8192, 8192)
+    n = shape[0] * shape[1]
+    x = dev(r.standard_normal(shape).astype(np.float32))
+    out = {}
+    tm = Timer()
+    for axes, label in (((0,), "axis0"), ((1,), "axis1"), ((0, 1), "full")):
+        kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+        g = dev(r.standard_normal(kshape if kshape else ()).astype(np.float32).reshape(kshape))
+        old = dev(r.standard_normal(shape).astype(np.float32))
+        for _ in range(iters):
+            tm.run(f"sum|{label}|fwd", lambda: K.reduce(_lib.R_SUM, x, axes, nt.float32))
+            tm.run(f"max|{label}|fwd", lambda: K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True))
+            tm.run(f"min|{label}|fwd", lambda: K.reduce(_lib.R_MIN, x, axes, nt.float32, want_aux=True))
+        _, idx, cnt = K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True)
+        gb = g.reshape(*[1 if i in axes else s for i, s in enumerate(shape)]).expand(*shape)
+        for _ in range(iters):
+            # sum backward, accumulate: old += broadcast(g)
+            tm.run(f"sum|{label}|bwd", lambda: K.inplace(_lib.ADD, old, gb))
+            tm.run(f"mean|{label}|bwd", lambda: K.reduce_bwd(_lib.R_MEAN, g, float(n // max(1, g.numel)), None, None, axes, shape, None))
+            tm.run(f"max|{label}|bwd", lambda: K.reduce_bwd(_lib.R_MAX, g, 1.0, idx, cnt, axes, shape, None))
+    nt.sync()
+    fwd_bytes = n * 4
+    bwd_bytes = {"sum": 2 * n * 4, "mean": n * 4, "max": n * 4}
+    tot_b = tot_ms = 0.0
+    for key, ds in tm.durations().items():
+        op, label, phase = key.split("|")
+        ds = ds[1:] if len(ds) > 1 else ds  # first call allocates
+        avg = sum(ds) / len(ds)
+        b = fwd_bytes if phase == "fwd" else bwd_bytes[op]
+        gbs = b / (avg * 1e-3) / 1e9
+        out[key] = {"ms": round(avg, 5), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        tot_b += b
+        tot_ms += avg
+    return {"per_kernel": out, "aggregate_GB/s": round(tot_b / (tot_ms * 1e-3) / 1e9, 1)}
+
+
+# ------------------------------------------------------- config 4: matmul
+
+
+def bench_matmul(iters: int = 5) -> dict:
+    r = np.random.default_rng(4)
+    res = {}
+    for (M, Kd, N) in ((4096, 4096, 4096), (8192, 1024, 4096)):
+        A = r.standard_normal((M, Kd)).astype(np.float32)
+        B = (r.standard_normal((Kd, N)) / np.sqrt(Kd)).astype(np.float32)
+        G = r.standard_normal((M, N)).astype(np.float32)
+        tb, tg = dev(B), dev(G)
+        for a_layout in ("contig", "transposed"):
+            ta = dev(A) if a_layout == "contig" else dev_T(A)
+            c, da, db = _fresh((M, N)), _fresh((M, Kd)), _fresh((Kd, N))
+            calls = [
+                ("fwd", ta, tb, c), ("dA", tg, tb.T, da), ("dB", ta.T, tg, db),
+            ]
+            tm = Timer()
+            for _ in range(iters + 1):
+                for name, x1, x2, o in calls:
+                    tm.run(name, lambda x1=x1, x2=x2, o=o: K.matmul_into(x1, x2, o, accumulate=False))
+            nt.sync()
+            flop = 2 * M * N * Kd
+            key = f"{M}x{Kd}x{N}|{a_layout}"
+            tot_ms = 0.0
+            entry = {}
+            for name, ds in tm.durations().items():
+                avg = sum(ds[1:]) / len(ds[1:])
+                tot_ms += avg
+                tf = flop / (avg * 1e-3) / 1e12
+                entry[name] = {"ms": round(avg, 4), "TFLOP/s": round(tf, 2),
+                               "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+            tf = 3 * flop / (tot_ms * 1e-3) / 1e12
+            entry["fwd+dA+dB"] = {"ms": round(tot_ms, 4), "TFLOP/s": round(tf, 2),
+                                  "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+            res[key] = entry
+    return res
+
+
+# ---------------------------------------------------------- config 5: MLP
+
+
+def bench_mlp(steps: int = 20) -> dict:
+    r = np.random.default_rng(5)
+    B, D_in = 8192, 1024
+    dims = [1024, 4096, 4096, 4096, 1000]
+    X = dev(r.standard_normal((B, D_in)).astype(np.float32))
+    T = dev(r.standard_normal((B, 1000)).astype(np.float32))
+    layers = []
+    for i in range(4):
+        lin = nn.Linear(dims[i], dims[i + 1])
+        w = (r.standard_normal((dims[i], dims[i + 1])) * np.sqrt(2.0 / dims[i])).astype(np.float32)
+        lin._W = dev(w)
+        lin._W.enable_grad()
+        layers.append(lin)
+    model = nn.Sequential(layers[0], nn.Tanh(), layers[1], nn.Sigmoid(), layers[2],
+                             nn.ReLU(), layers[3])
+    opt = nn.GradientDescent(model.parameters(), lr=1e-3)
+    losses = []
+    times = []
+    for s in range(steps):
+        e0, e1 = _lib.Event(), _lib.Event()
+        e0.record()
+        opt.zero_grad()
+        y = model(X)
+        loss = nt.mean((y - T) ** 2)
+        loss.backward()
+        opt.step()
+        e1.record()
+        losses.append(loss)
+        times.append((e0, e1))
+    nt.sync()
+    ms = [a.elapsed_ms(b) for a, b in times]
+    trace = [float(lo.cpu().item()) for lo in losses]
+    steady = ms[2:] if len(ms) > 3 else ms
+    avg = sum(steady) / len(steady)
+    flop = 1_988_032_987_136  # per step; layer-1 dX is not computed (X needs no grad)
+    return {"step/s": round(1000.0 / avg, 3), "ms_per_step": round(avg, 3),
+            "matmul_TFLOP/s": round(flop / (avg * 1e-3) / 1e12, 2),
+            "loss_trace": [round(v, 7) for v in trace], "steps": steps}
+
+
+# ------------------------------------------------------------ CPU baseline
+
+
+def cpu_baseline(rows: int = 1024) -> dict:
+    """The oracle (reference CPU kernels restated, single thread) on a
+    [rows, 4096] sample of the config-2 sweep: forward, then the reference's
+    backward composition and the engine's accumulate, both layouts."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    r = np.random.default_rng(7)
+    shape = (rows, 4096)
+    n = rows * 4096
+    total_bytes = 0
+    t0 = time.perf_counter()
+    for layout in ("contig", "transposed"):
+        mk = (lambda a: a) if layout == "contig" else (lambda a: np.ascontiguousarray(a.T).T)
+        for name, op in (("add", O.ADD), ("sub", O.SUB), ("mul", O.MUL), ("truediv", O.DIV)):
+            a = mk(r.standard_normal(shape).astype(np.float32))
+            b = mk((r.uniform(0.5, 2, shape) if name == "truediv" else r.standard_normal(shape)).astype(np.float32))
+            g = r.standard_normal(shape).astype(np.float32)
+            O.binary(op, a, b)
+            ga, gb = O.bwd_binary(op, g, a, b)
+            O.accumulate(np.ones(shape, np.float32), ga)
+            O.accumulate(np.ones(shape, np.float32), gb)
+            total_bytes += (ew_bytes(name, "fwd") + ew_bytes(name, "bwd")) * n // N_ELEM
+        for name, op, dom, saved, e in UNARY_OPS:
+            x = mk((r.standard_normal(shape) if dom is None else r.uniform(dom[0], dom[1], shape)).astype(np.float32))
+            g = r.standard_normal(shape).astype(np.float32)
+            oop = {"neg": O.NEG, "exp": O.EXP, "log": O.LOG, "sqrt": O.SQRT, "pow": O.POW,
+                   "relu": O.RELU, "sigmoid": O.SIGMOID, "tanh": O.TANH}[name]
+            y = O.unary(oop, x, e)
+            chain = {"neg": lambda: O.bwd_neg(g), "exp": lambda: O.bwd_exp(g, y),
+                     "log": lambda: O.bwd_log(g, x), "sqrt": lambda: O.bwd_sqrt(g, y),
+                     "pow": lambda: O.bwd_pow(g, x, 2.5), "relu": lambda: O.bwd_relu(g, y),
+                     "sigmoid": lambda: O.bwd_sigmoid(g, y), "tanh": lambda: O.bwd_tanh(g, y)}[name]
+            O.accumulate(np.ones(shape, np.float32), chain())
+            total_bytes += (ew_bytes(name, "fwd") + ew_bytes(name, "bwd")) * n // N_ELEM
+    dt = time.perf_counter() - t0
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(total_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"config-2 sweep on [{rows},4096] (1/{4096 // rows} of the workload), "
+                      f"forward + reference backward composition + accumulate, both layouts, "
+                      f"single thread, {dt:.1f} s",
+            "host_cpu": cpu, "host_nproc": os.cpu_count()}
+
+
+# -------------------------------------------------------------------- main
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--parts", default="all", help="all | none | comma list of red,mm,mlp,cpu")
+    ap.add_argument("--mlp-steps", type=int, default=20)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for {max(args.gpus, world)}); "
+              "this build has no multi-GPU path.", file=sys.stderr)
+        return 2
+    if not nt.is_available():
+        print("no HIP device / libnt.so", file=sys.stderr)
+        return 1
+    parts = {"red", "mm", "mlp", "cpu"} if args.parts == "all" else (
+        set() if args.parts == "none" else set(args.parts.split(",")))
+
+    ew = bench_elementwise(args.steps, args.warmup)
+    value = ew["step_bytes"] / (ew["ms_per_step"] * 1e-3) / 1e9
+    # dominant kernel: the one with the largest share of the sweep's time
+    dom_key, dom = max(ew["per_kernel"].items(), key=lambda kv: kv[1]["ms"])
+    line = {
+        "metric": "elementwise fwd+bwd HBM GB/s (config-2 sweep)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ew["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) / U[a,b] per config 2)",
+        "config": {"workload": "config 2: 12 elementwise ops fwd + fused bwd (accumulate), "
+                               "2^24 fp32 elements [4096,4096], contiguous and .T views",
+                   "elements": N_ELEM, "kernels_per_step": len(ew["per_kernel"])},
+        "baseline_metric": BASELINE_METRIC,
+        "roofline": {"bound": "hbm", "kernel": dom_key, "achieved": dom["GB/s"],
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
+                     "traffic": None, "bytes_per_launch": dom["bytes"]},
+        "sweep_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        "parts": {"elementwise_per_kernel": ew["per_kernel"]},
+    }
+    if "red" in parts:
+        line["parts"]["reductions"] = bench_reductions()
+    if "mm" in parts:
+        line["parts"]["matmul"] = bench_matmul()
+    if "mlp" in parts:
+        line["parts"]["mlp"] = bench_mlp(args.mlp_steps)
+    if "cpu" in parts:
+        line["cpu_baseline"] = cpu_baseline()
+    else:
+        line["cpu_baseline"] = None
+    line["host"] = platform.node()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

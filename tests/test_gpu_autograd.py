@@ -1,0 +1,325 @@
+"""The Tensor / autograd API on the GPU: the reference's autograd behaviours
+(tests/test_autograd.py), every op's gradient through the engine against the
+oracle's restatement of the reference compositions, and the MLP configs.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import assert_bitexact, assert_rel, dev, dev_T, host, rng, seed_of
+
+import nanotorch_amd as nt
+from nanotorch_amd import nn
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KA = json.load(open(os.path.join(HERE, "golden", "known_answers.json")))
+
+
+def T(v, **kw):
+    return nt.tensor(v, device="cuda", **kw)
+
+
+# ------------------------------------------------ reference behaviours
+
+
+def test_backward_known_answers(gpu):
+    x = T(1.0, requires_grad=True)
+    loss = 3 * x
+    loss.backward()
+    assert loss.grad is None and x.grad.cpu().item() == 3.0
+
+    x = T(1.0, requires_grad=True)
+    y = 3 * x
+    loss = y.exp()
+    loss.backward()
+    assert y.grad is None
+    assert abs(x.grad.cpu().item() - 60.2566) < 1e-3
+
+    x1, x2 = T(1.0, requires_grad=True), T(5.0, requires_grad=True)
+    (x1 * x2).log().backward()
+    assert abs(x1.grad.cpu().item() - 1.0) < 1e-6 and abs(x2.grad.cpu().item() - 0.2) < 1e-6
+
+    x1, x2 = T([1.0, 5.0], requires_grad=True), T([5.0, 1.0], requires_grad=True)
+    (x1 * x2).log().sum().backward()
+    assert np.allclose(host(x1.grad), [1.0, 0.2]) and np.allclose(host(x2.grad), [0.2, 1.0])
+
+    x = T([[1.0, 2.0], [2.0, 1.0]], requires_grad=True)
+    x.sum(axis=0).sum().backward()
+    assert host(x.grad).tolist() == [[1.0, 1.0], [1.0, 1.0]]
+
+    x = T([[1.0, 2.0], [2.0, 1.0]], requires_grad=True)
+    x.sum(axis=0, keepdim=True).sum().backward()
+    assert host(x.grad).tolist() == [[1.0, 1.0], [1.0, 1.0]]
+
+    x = T([[0.0, 0.0, 0.0], [0.0, 0.0, 0.0]], requires_grad=True)
+    g = nt.arange(6, device="cuda").reshape(3, 2)
+    (x.T * g).sum().backward()
+    assert host(x.grad).tolist() == [[0, 2, 4], [1, 3, 5]]
+
+    x = T([1.0, 2.0], requires_grad=True)
+    a = x.exp()
+    ((a * 2) + (a * 3)).sum().backward()
+    assert np.allclose(host(x.grad), [5 * math.e, 5 * math.e**2], rtol=1e-6)
+
+
+def test_grad_state_and_guards(gpu):
+    assert not T(0.0).requires_grad
+    with pytest.raises(RuntimeError):
+        T(1, dtype=nt.int64, requires_grad=True)
+    x2 = T([5.0, 1.0], requires_grad=True)
+    with pytest.raises(RuntimeError):
+        x2 *= 1.5
+    x = T([5.0, 1.0], requires_grad=True)
+    y = x.exp()
+    y += 3
+    with pytest.raises(RuntimeError):
+        y.sum().backward()
+    x = T([1.0, 2.0], requires_grad=True)
+    y = 2 * x
+    z = 3 * y
+    y += 2
+    with pytest.raises(RuntimeError):
+        z.backward()  # non-scalar and a modified saved tensor
+    with nt.no_grad():
+        assert (2 * x).grad_fn is None
+    with pytest.raises(RuntimeError):
+        T([1.0, 2.0], requires_grad=True).backward()
+
+
+def test_inplace_semantics(gpu):
+    t = T([1.0, 2.0, 3.0])
+    st = t.storage
+    v0 = t.version
+    t += 1
+    assert t.storage is st and t.version == v0 + 1
+    assert host(t).tolist() == [2.0, 3.0, 4.0]
+    base = T([[1.0, 2.0], [3.0, 4.0]])
+    row = base[1]
+    row *= 10
+    assert host(base).tolist() == [[1.0, 2.0], [30.0, 40.0]]
+    s = T([1.0, 2.0])
+    s += s
+    assert host(s).tolist() == [2.0, 4.0]
+    with pytest.raises(RuntimeError):
+        T([1.0, 2.0]) + T([1.0, 2.0, 3.0])
+    with pytest.raises(ValueError):
+        T([True]).__truediv__(T([True]))
+
+
+# ---------------------------------------- op gradients through the engine
+
+UNARY_API = [
+    ("exp", lambda t: t.exp(), O.EXP, O.bwd_exp, (-4, 4), "out"),
+    ("log", lambda t: t.log(), O.LOG, O.bwd_log, (0.1, 4), "in"),
+    ("sqrt", lambda t: nt.sqrt(t), O.SQRT, O.bwd_sqrt, (0.1, 4), "out"),
+    ("tanh", lambda t: nt.tanh(t), O.TANH, O.bwd_tanh, None, "out"),
+    ("sigmoid", lambda t: nt.sigmoid(t), O.SIGMOID, O.bwd_sigmoid, None, "out"),
+    ("relu", lambda t: nt.relu(t), O.RELU, O.bwd_relu, None, "out"),
+    ("neg", lambda t: -t, None, lambda g, s: O.bwd_neg(g), (-4, 4), None),
+    ("pow", lambda t: t ** 2.5, None, lambda g, x: O.bwd_pow(g, x, 2.5), (0.1, 4), "in"),
+]
+
+
+@pytest.mark.parametrize("layout", ["contig", "transposed"])
+@pytest.mark.parametrize("name,fn,oop,chain,dom,saved", UNARY_API)
+def test_unary_grad_api(gpu, name, fn, oop, chain, dom, saved, layout):
+    """y = f(x) used twice: x.grad = chain(g1) then += chain(g2)."""
+    r = rng(seed_of("uapi", name, layout))
+    shape = (96, 160)
+    a = (r.standard_normal(shape) if dom is None else r.uniform(dom[0], dom[1], shape)).astype(np.float32)
+    g1 = r.standard_normal(shape).astype(np.float32)
+    g2 = r.standard_normal(shape).astype(np.float32)
+    x = dev(a) if layout == "contig" else dev_T(a)
+    x.enable_grad()
+    y = fn(x)
+    loss = (y * dev(g1)).sum() + (fn(x) * dev(g2)).sum()
+    loss.backward()
+    if oop is not None:
+        s = O.unary(oop, a) if saved == "out" else a
+    elif name == "pow":
+        s = a
+    else:
+        s = None
+    t1, t2 = chain(g1, s), chain(g2, s)
+    want = O.accumulate(t1, t2)
+    scale = np.abs(t1).astype(np.float64) + np.abs(t2)
+    if name == "tanh":
+        scale = (np.abs(g1) + np.abs(g2)) * (1 + s.astype(np.float64) ** 2)
+    got = host(x.grad)
+    if name in ("log", "sqrt", "tanh", "pow"):
+        assert_rel(got, want, 1e-6, name, scale=scale)
+    else:
+        assert_bitexact(got, want, name)
+
+
+@pytest.mark.parametrize("name,op", [("add", O.ADD), ("sub", O.SUB), ("mul", O.MUL), ("div", O.DIV)])
+def test_binary_grad_api_with_broadcast(gpu, name, op):
+    r = rng(seed_of("bapi", name))
+    a = r.standard_normal((64, 48)).astype(np.float32)
+    b = (r.uniform(0.5, 2, (48,)) if name == "div" else r.standard_normal((48,))).astype(np.float32)
+    g = r.standard_normal((64, 48)).astype(np.float32)
+    x1, x2 = dev(a), dev(b)
+    x1.enable_grad()
+    x2.enable_grad()
+    f = {"add": lambda u, v: u + v, "sub": lambda u, v: u - v,
+         "mul": lambda u, v: u * v, "div": lambda u, v: u / v}[name]
+    (f(x1, x2) * dev(g)).sum().backward()
+    bb = np.ascontiguousarray(np.broadcast_to(b, a.shape))
+    ga, gb_full = O.bwd_binary(op, g, a, bb)
+    gb = O.reduce(O.R_SUM, gb_full, (0,), np.float32)  # unbroadcast
+    sa = np.abs(ga).astype(np.float64) + 1e-30
+    assert_rel(host(x1.grad), ga, 1e-6, name, scale=sa)
+    sb = O.reduce(O.R_SUM, np.abs(gb_full).astype(np.float64), (0,), np.float64)
+    assert_rel(host(x2.grad), gb, 1e-5, name + " b", scale=sb)
+
+
+def test_duplicate_input(gpu):
+    r = rng(12)
+    a = r.standard_normal((50, 70)).astype(np.float32)
+    g = r.standard_normal((50, 70)).astype(np.float32)
+    x = dev(a)
+    x.enable_grad()
+    ((x * x) * dev(g)).sum().backward()
+    ga, gb = O.bwd_binary(O.MUL, g, a, a)
+    assert_bitexact(host(x.grad), O.accumulate(ga, gb), "x*x")
+
+
+def test_grad_aliasing_is_not_shared(gpu):
+    """z = a + b hands the same upstream gradient to a and b; a later
+    contribution to a must not change b's gradient."""
+    a = T([1.0, 2.0], requires_grad=True)
+    b = T([3.0, 4.0], requires_grad=True)
+    loss = (a + b).sum() + (a * 2).sum()
+    loss.backward()
+    assert host(a.grad).tolist() == [3.0, 3.0]
+    assert host(b.grad).tolist() == [1.0, 1.0]
+
+
+@pytest.mark.parametrize("op", ["max", "min"])
+def test_select_grad_api(gpu, op):
+    r = rng(seed_of("sel", op))
+    a = r.integers(-5, 5, (40, 30)).astype(np.float32)
+    g = r.standard_normal(40).astype(np.float32)
+    x = dev(a)
+    x.enable_grad()
+    m = x.max(axis=1) if op == "max" else x.min(axis=1)
+    assert_bitexact(host(m), (a.max(1) if op == "max" else a.min(1)), op)
+    (m * dev(g)).sum().backward()
+    want = O.sel_bwd(O.R_MAX if op == "max" else O.R_MIN, g, a, (1,))
+    assert_bitexact(host(x.grad), want, op + " bwd")
+
+
+def test_mean_and_sum_grad_api(gpu):
+    r = rng(13)
+    a = r.standard_normal((33, 21)).astype(np.float32)
+    x = dev(a)
+    x.enable_grad()
+    (x.mean(axis=0).sum() + x.sum()).backward()
+    g_mean = O.binary(O.DIV, np.ones((33, 21), np.float32),
+                      np.broadcast_to(O.scalar(33, np.float32), (33, 21)))
+    assert_bitexact(host(x.grad), O.accumulate(g_mean, np.ones((33, 21), np.float32)), "mean+sum")
+
+
+def test_matmul_variants_api(gpu):
+    r = rng(14)
+    assert (nt.arange(5, device="cuda") @ nt.arange(5, device="cuda")).cpu().tolist() == 30
+    for s1, s2 in (((5, 7), (7,)), ((7,), (7, 3)), ((2, 3, 5, 7), (7, 4)), ((3, 5, 7), (2, 1, 7, 4))):
+        a = r.standard_normal(s1).astype(np.float32)
+        b = r.standard_normal(s2).astype(np.float32)
+        x1, x2 = dev(a), dev(b)
+        x1.enable_grad()
+        x2.enable_grad()
+        y = x1 @ x2
+        want = np.matmul(a.astype(np.float64), b.astype(np.float64))
+        assert host(y).shape == want.shape
+        assert np.allclose(host(y), want, rtol=1e-4, atol=1e-4)
+        y.sum().backward()
+        # L = sum(x1 @ x2) is linear in each operand: dL/dx_i = L(e_i).
+        A, B = a.astype(np.float64), b.astype(np.float64)
+        for arr, other, first, got in ((A, B, True, x1.grad), (B, A, False, x2.grad)):
+            grad = np.zeros(arr.size)
+            for i in range(arr.size):
+                e = np.zeros(arr.size)
+                e[i] = 1.0
+                e = e.reshape(arr.shape)
+                grad[i] = np.matmul(e, other).sum() if first else np.matmul(other, e).sum()
+            assert np.allclose(host(got), grad.reshape(arr.shape), rtol=1e-4, atol=1e-4), (s1, s2)
+
+
+# --------------------------------------------------------------- MLPs
+
+
+def _mlp_params(r, dims):
+    return [((r.standard_normal((dims[i], dims[i + 1])) * np.sqrt(2.0 / dims[i])).astype(np.float32),
+             np.zeros(dims[i + 1], np.float32)) for i in range(len(dims) - 1)]
+
+
+def _run_mlp(params, x, t, acts, lr, steps):
+    lins = []
+    mods = []
+    for i, (W, b) in enumerate(params):
+        lin = nn.Linear(W.shape[0], W.shape[1])
+        lin._W = dev(W)
+        lin._W.enable_grad()
+        lin._b = dev(b)
+        lin._b.enable_grad()
+        lins.append(lin)
+        mods.append(lin)
+        if i < len(acts):
+            mods.append({"relu": nn.ReLU(), "tanh": nn.Tanh(), "sigmoid": nn.Sigmoid()}[acts[i]])
+    model = nn.Sequential(*mods)
+    opt = nn.GradientDescent(model.parameters(), lr=lr)
+    X, Tt = dev(x), dev(t)
+    losses = []
+    for _ in range(steps):
+        opt.zero_grad()
+        loss = nt.mean((model(X) - Tt) ** 2)
+        loss.backward()
+        opt.step()
+        losses.append(float(loss.cpu().item()))
+    return losses, [(host(l._W), host(l._b)) for l in lins]
+
+
+def test_config1_mlp_vs_oracle(gpu):
+    """Config 1: X [64,784] ~ N(0,1), one-hot targets, Linear 784->256 ->
+    ReLU -> Linear 256->10, MSE, SGD lr=0.01, 100 steps; per-step loss and
+    final weights against the oracle's step (rel 1e-4 / 1e-3)."""
+    r = rng(2024)
+    x = r.standard_normal((64, 784)).astype(np.float32)
+    labels = r.integers(0, 10, 64)
+    t = np.eye(10, dtype=np.float32)[labels]
+    params = _mlp_params(r, [784, 256, 10])
+    got_losses, got_params = _run_mlp([(W.copy(), b.copy()) for W, b in params], x, t, ["relu"], 0.01, 100)
+    ref = [(W.copy(), b.copy()) for W, b in params]
+    ref_losses = [float(O.mlp_step(ref, x, t, ["relu"], 0.01)) for _ in range(100)]
+    for i, (g, w) in enumerate(zip(got_losses, ref_losses)):
+        assert abs(g - w) <= 1e-4 * abs(w), (i, g, w)
+    assert got_losses[-1] < got_losses[0]
+    for (gW, gb), (rW, rb) in zip(got_params, ref):
+        assert np.allclose(gW, rW, rtol=1e-3, atol=1e-5)
+        assert np.allclose(gb, rb, rtol=1e-3, atol=1e-5)
+
+
+def test_config5_mlp_shape_scaled_vs_oracle(gpu):
+    """Config 5's network (tanh / sigmoid / relu, 4 layers) at 1/8 width and
+    batch, 5 SGD steps of lr 1e-3: losses against the oracle (rel 1e-4)."""
+    r = rng(55)
+    dims = [128, 512, 512, 512, 125]
+    x = r.standard_normal((1024, 128)).astype(np.float32)
+    t = r.standard_normal((1024, 125)).astype(np.float32)
+    params = _mlp_params(r, dims)
+    acts = ["tanh", "sigmoid", "relu"]
+    got, _ = _run_mlp([(W.copy(), b.copy()) for W, b in params], x, t, acts, 1e-3, 5)
+    ref = [(W.copy(), b.copy()) for W, b in params]
+    want = [float(O.mlp_step(ref, x, t, acts, 1e-3)) for _ in range(5)]
+    for g, w in zip(got, want):
+        assert abs(g - w) <= 1e-4 * abs(w), (g, w)
