@@ -22,6 +22,9 @@ class Dtype(enum.IntEnum):
     Float32 = 3
     Float64 = 4
 
+    def __bool__(self) -> bool:  # every dtype is truthy, Bool (0) included
+        return True
+
 
 _CTYPES = {
     Dtype.Bool: ctypes.c_bool,

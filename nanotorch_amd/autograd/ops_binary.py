@@ -176,6 +176,7 @@ class MatmulOp(Function):
 
     def backward(self, grad_out: Tensor) -> tuple[Tensor, ...]:
         x1, x2 = self.saved_tensors
+        x2_shape = x2.shape
         x1_m = x1.expand(*self._shape1)
         if x2.ndim == 1 and self._shape2[-2:] == (x2.shape[0], 1):
             x2 = x2.reshape(x2.shape[0], 1)
@@ -185,9 +186,11 @@ class MatmulOp(Function):
             self._shape1[-2],
             self._shape2[-1],
         )
+        # The gradient of a 1-D right operand is reshaped back to (k,); the
+        # reference keeps the (k, 1) column it multiplied with.
         return (
             unbroadcast(grad_out @ x2_m.transpose(-2, -1), x1.shape).reshape(*x1.shape),
-            unbroadcast(x1_m.transpose(-2, -1) @ grad_out, x2.shape).reshape(*x2.shape),
+            unbroadcast(x1_m.transpose(-2, -1) @ grad_out, x2.shape).reshape(*x2_shape),
         )
 
     def fused_ok(self) -> bool:

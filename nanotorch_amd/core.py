@@ -459,7 +459,8 @@ def _extract_tensor_data(data, target_device: Device, user_dtype: Dtype | None):
             raise TypeError(f"Unsupported tensor element type: {type(node)}")
 
     rec(data, 0)
-    auto_dtype = auto_dtype or Dtype.Float32
+    if auto_dtype is None:
+        auto_dtype = Dtype.Float32
     final = Dtype(user_dtype) if user_dtype is not None else auto_dtype
     if is_bool(final):
         values = [bool(x) for x in flat]

@@ -70,15 +70,13 @@ template <class O, bool IS_MAX> struct SelAcc {
     else
       return a < b;
   }
+  // Branch-free update (selects, no divergent control flow).
   __device__ __forceinline__ void add(O x, int64_t jj) {
-    if (better(x, v)) {
-      v = x;
-      j = jj;
-      c = 1;
-    } else if (x == v) {
-      j = jj < j ? jj : j;
-      c += 1;
-    }
+    const bool b = better(x, v);
+    const bool e = (x == v);
+    j = b ? jj : ((e && jj < j) ? jj : j);
+    c = b ? 1 : c + (e ? 1 : 0);
+    v = b ? x : v;
   }
   __device__ __forceinline__ void merge(const SelAcc &o) {
     if (better(o.v, v)) {
@@ -185,10 +183,24 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
   Acc a;
   a.init();
   using V = VecT<T, VEC>;
-  for (int64_t j = j0 + int64_t(threadIdx.x) * VEC; j < j1;
-       j += int64_t(RED_THREADS) * VEC) {
+  // Four independent vector loads in flight per work-item, then the tail.
+  constexpr int UR = 4;
+  const int64_t step = int64_t(RED_THREADS) * VEC;
+  int64_t j = j0 + int64_t(threadIdx.x) * VEC;
+  for (; j + (UR - 1) * step + VEC <= j1; j += UR * step) {
+    V v[UR];
+#pragma unroll
+    for (int u = 0; u < UR; ++u)
+      v[u] = vload<true, T, VEC>(row + j + u * step);
+#pragma unroll
+    for (int u = 0; u < UR; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        a.add(static_cast<O>(v[u].v[i]), j + u * step + i);
+  }
+  for (; j < j1; j += step) {
     if (VEC > 1 && j + VEC <= j1) {
-      const V v = *reinterpret_cast<const V *>(row + j);
+      const V v = vload<true, T, VEC>(row + j);
 #pragma unroll
       for (int i = 0; i < VEC; ++i)
         a.add(static_cast<O>(v.v[i]), j + i);
@@ -225,8 +237,22 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
     a[i].init();
   using V = VecT<T, VEC>;
   if (k0 + VEC <= K) {
-    for (int64_t j = j0 + w; j < j1; j += RED_WAVES) {
-      const V v = *reinterpret_cast<const V *>(x + j * sd + k0);
+    // Four rows in flight per work-item, then the tail.
+    constexpr int UR = 4;
+    int64_t j = j0 + w;
+    for (; j + (UR - 1) * RED_WAVES < j1; j += UR * RED_WAVES) {
+      V v[UR];
+#pragma unroll
+      for (int u = 0; u < UR; ++u)
+        v[u] = vload<true, T, VEC>(x + (j + u * RED_WAVES) * sd + k0);
+#pragma unroll
+      for (int u = 0; u < UR; ++u)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+          a[i].add(static_cast<O>(v[u].v[i]), j + u * RED_WAVES);
+    }
+    for (; j < j1; j += RED_WAVES) {
+      const V v = vload<true, T, VEC>(x + j * sd + k0);
 #pragma unroll
       for (int i = 0; i < VEC; ++i)
         a[i].add(static_cast<O>(v.v[i]), j);
@@ -556,6 +582,110 @@ __global__ __launch_bounds__(256) void sel_bwd_kernel(
   }
 }
 
+// Max/min backward when gx is contiguous and the reduced axes are the
+// trailing (MODE 0: k = i / C, j = i % C), leading (MODE 1: k = i % C,
+// j = i / C) or all (MODE 2: k = 0, j = i) dims in increasing order.  Each
+// work-item writes 4 consecutive elements with one 16-byte store.
+template <class T, bool ACC, int MODE>
+__global__ __launch_bounds__(256) void sel_bwd_vec_kernel(
+    const T *__restrict__ g, const int64_t *__restrict__ idx,
+    const int32_t *__restrict__ cnt, T *gx, FastDivU32 fdC, uint32_t C,
+    int64_t n4) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t q = int64_t(blockIdx.x) * 256 + threadIdx.x; q < n4;
+       q += stride) {
+    VecT<T, 4> o;
+    VecT<T, 4> old;
+    if constexpr (ACC)
+      old = vload<true, T, 4>(gx + 4 * q);
+    const uint32_t i0 = uint32_t(4 * q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t i = i0 + e;
+      int64_t k, j;
+      if constexpr (MODE == 0) {
+        const uint32_t qq = fdC.div(i);
+        k = qq;
+        j = i - qq * C;
+      } else if constexpr (MODE == 1) {
+        const uint32_t qq = fdC.div(i);
+        k = i - qq * C;
+        j = qq;
+      } else {
+        k = 0;
+        j = i;
+      }
+      const bool sel = (j == idx[k]) && (cnt[k] == 1);
+      const T t = g[k] * (sel ? T(1) : T(0));
+      if constexpr (ACC)
+        o.v[e] = old.v[e] + t;
+      else
+        o.v[e] = t;
+    }
+    *reinterpret_cast<VecT<T, 4> *>(gx + 4 * q) = o;
+  }
+}
+
+// Max/min backward on a contiguous [Rr, Cc] gx, Cc % 4 == 0.  MODE 0: slice
+// k = row, reduced index j = column (trailing axes reduced); MODE 1: k =
+// column, j = row (leading axes reduced).  Lane l of block (bx, by) owns
+// columns 4 * (64 bx + l) .. +3 and the waves walk rows by * rpb + w, +4, ...
+// The slice's (g, idx, count) is loaded once per row (MODE 0) or once per
+// work-item (MODE 1), so the kernel is a plain 16-byte streaming write.
+template <class T, bool ACC, int MODE>
+__global__ __launch_bounds__(256) void sel_bwd_2d_kernel(
+    const T *__restrict__ g, const int64_t *__restrict__ idx,
+    const int32_t *__restrict__ cnt, T *gx, int64_t Rr, int64_t Cc,
+    int64_t rpb) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = (int64_t(blockIdx.x) * 64 + lane) * 4;
+  const int64_t r0 = int64_t(blockIdx.y) * rpb;
+  const int64_t r1 = r0 + rpb < Rr ? r0 + rpb : Rr;
+  if (c >= Cc)
+    return;
+  T gk[4];
+  int64_t ik[4];
+  bool ok[4];
+  if constexpr (MODE == 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gk[e] = g[c + e];
+      ik[e] = idx[c + e];
+      ok[e] = cnt[c + e] == 1;
+    }
+  }
+  for (int64_t r = r0 + w; r < r1; r += RED_WAVES) {
+    T *p = gx + r * Cc + c;
+    VecT<T, 4> o;
+    VecT<T, 4> old;
+    if constexpr (ACC)
+      old = vload<true, T, 4>(p);
+    if constexpr (MODE == 0) {
+      const T gr = g[r];
+      const int64_t ir = idx[r];
+      const bool okr = cnt[r] == 1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const T t = gr * ((okr && c + e == ir) ? T(1) : T(0));
+        if constexpr (ACC)
+          o.v[e] = old.v[e] + t;
+        else
+          o.v[e] = t;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const T t = gk[e] * ((ok[e] && r == ik[e]) ? T(1) : T(0));
+        if constexpr (ACC)
+          o.v[e] = old.v[e] + t;
+        else
+          o.v[e] = t;
+      }
+    }
+    *reinterpret_cast<VecT<T, 4> *>(p) = o;
+  }
+}
+
 template <class T, bool ACC> struct BcastBwd {
   T scale;
   bool divide;
@@ -709,6 +839,78 @@ int nt_reduce_bwd(int32_t op, const nt_view *g, double scale, const nt_view *idx
         numel(idx) != K || numel(count) != K || !is_contiguous(idx) ||
         !is_contiguous(count))
       fail(NT_ERR_RUNTIME, "reduction_bwd: bad idx/count");
+    // Vector path: contiguous, aligned gx whose reduced axes are the
+    // trailing, leading or all dims, in increasing order.
+    {
+      bool inc = true;
+      for (int i = 1; i < naxes; ++i)
+        if (axes[i] != axes[i - 1] + 1)
+          inc = false;
+      const bool trailing = inc && naxes > 0 && axes[naxes - 1] == gx->ndim - 1;
+      const bool leading = inc && naxes > 0 && axes[0] == 0;
+      const size_t es = dtype_size(gx->dtype);
+      const bool ok = is_contiguous(gx) && n % 4 == 0 &&
+                      n < (int64_t(1) << 32) &&
+                      reinterpret_cast<uintptr_t>(
+                          static_cast<char *>(gx->data) + gx->offset * es) %
+                              (4 * es) == 0;
+      int mode = -1;
+      int64_t Cdim = 1;
+      if (ok && trailing && leading) {
+        mode = 2;
+      } else if (ok && trailing && D % 4 == 0) {
+        mode = 0;
+        Cdim = D;
+      } else if (ok && leading && K % 4 == 0) {
+        mode = 1;
+        Cdim = K;
+      }
+      if (mode >= 0) {
+        const FastDivU32 fd{static_cast<uint32_t>(Cdim)};
+        const int64_t n4 = n / 4;
+        const int64_t blocks = std::max<int64_t>(
+            1, std::min<int64_t>(ceil_div(n4, 256), int64_t(device_cu_count()) * 16));
+        dispatch_float(g->dtype, [&]<class T>() {
+          const T *gp = typed_ptr<const T>(g);
+          const int64_t *ip = typed_ptr<const int64_t>(idx);
+          const int32_t *cp = typed_ptr<const int32_t>(count);
+          T *xp = typed_ptr<T>(gx);
+          const dim3 grid{unsigned(blocks), 1u, 1u};
+          hipStream_t st = stream();
+          const uint32_t Cu = uint32_t(Cdim);
+          if (mode == 2) {
+            if (acc)
+              sel_bwd_vec_kernel<T, true, 2>
+                  <<<grid, 256, 0, st>>>(gp, ip, cp, xp, fd, Cu, n4);
+            else
+              sel_bwd_vec_kernel<T, false, 2>
+                  <<<grid, 256, 0, st>>>(gp, ip, cp, xp, fd, Cu, n4);
+          } else {
+            const int64_t Cc = Cdim, Rr = n / Cdim;
+            const int64_t bx = ceil_div(Cc, 256);
+            const int64_t target = int64_t(device_cu_count()) * 8;
+            const int64_t by = std::max<int64_t>(
+                1, std::min<int64_t>(ceil_div(target, bx), ceil_div(Rr, 16)));
+            const int64_t rpb = ceil_div(Rr, by);
+            const dim3 g2{unsigned(bx), unsigned(ceil_div(Rr, rpb)), 1u};
+#define NT_SEL2D(ACC, MODE)                                                    \
+  sel_bwd_2d_kernel<T, ACC, MODE><<<g2, 256, 0, st>>>(gp, ip, cp, xp, Rr, Cc, \
+                                                      rpb)
+            if (acc && mode == 0)
+              NT_SEL2D(true, 0);
+            else if (acc)
+              NT_SEL2D(true, 1);
+            else if (mode == 0)
+              NT_SEL2D(false, 0);
+            else
+              NT_SEL2D(false, 1);
+#undef NT_SEL2D
+          }
+          NT_LAUNCH_CHECK();
+        });
+        return;
+      }
+    }
     SelBwdDesc dsc{};
     dsc.ndim = gx->ndim;
     const bool idx32 = n < (int64_t(1) << 32);

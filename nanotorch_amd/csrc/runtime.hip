@@ -5,11 +5,12 @@
 // checks), src/cpp/allocator.{h,cpp} (caching allocator), src/cpp/storage.cpp
 // (allocate/to/clone), src/cpp/factory.cu (fills) and src/cpp/random.h (RNG).
 #include <algorithm>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <random>
 
-#include "nt_internal.h"
+#include "ew_engine.h"
 
 namespace nt {
 
@@ -161,6 +162,14 @@ void ensure_init() {
   NT_HIP_CHECK(hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking));
   r.available = true;
   r.initialised = true;
+}
+
+bool ew_nontemporal() {
+  static const bool on = [] {
+    const char *e = std::getenv("NT_NONTEMPORAL");
+    return !(e && e[0] == '0');
+  }();
+  return on;
 }
 
 hipStream_t stream() { return rt().stream; }
