@@ -30,19 +30,16 @@
 // `old + term` with one rounding, the reference's add_inplace
 // (src/cpp/ops/inplace_ops.cu:75).
 #include "ew_engine.h"
+#include "nt_math.h"
 
 namespace nt {
-
-__device__ __forceinline__ float b_pow(float a, float e) { return powf(a, e); }
-__device__ __forceinline__ double b_pow(double a, double e) {
-  return pow(a, e);
-}
 
 template <int OP> constexpr bool unary_uses_saved() { return OP != NT_NEG; }
 
 template <int OP, class T, bool ACC> struct UnaryBwd {
   T e;   // pow exponent (already rounded as the reference's fp32 tensor)
   T em1; // e - 1 formed in fp32
+  PowPlan plan; // evaluation plan for pow(x, em1)
   static constexpr bool S = unary_uses_saved<OP>();
   static constexpr int NI = 1 + (S ? 1 : 0) + (ACC ? 1 : 0);
   __device__ __forceinline__ void operator()(const T (&x)[NI],
@@ -65,7 +62,7 @@ template <int OP, class T, bool ACC> struct UnaryBwd {
     else if constexpr (OP == NT_RELU)
       t = g * (s > T(0) ? T(1) : T(0));
     else
-      t = (g * e) * b_pow(s, em1);
+      t = (g * e) * pow_planned(s, em1, plan);
     if constexpr (ACC)
       y[0] = x[NI - 1] + t;
     else
@@ -132,7 +129,8 @@ void run_unary_bwd(const nt_view *g, const nt_view *s, double scalar,
                    const nt_view *gx) {
   using F = UnaryBwd<OP, T, ACC>;
   const float ef = float(scalar);
-  F f{T(scalar), T(ef - 1.0f)};
+  const T em1 = T(ef - 1.0f);
+  F f{T(scalar), em1, make_pow_plan(double(em1))};
   const nt_view *ins[F::NI];
   int k = 0;
   ins[k++] = g;

@@ -12,6 +12,7 @@
 // (-fhip-fp32-correctly-rounded-divide-sqrt) and nothing is contracted into
 // FMA (-ffp-contract=off), so +,-,*,/,sqrt match the host bit for bit.
 #include "ew_engine.h"
+#include "nt_math.h"
 
 namespace nt {
 
@@ -25,10 +26,6 @@ __device__ __forceinline__ float d_sqrt(float a) { return sqrtf(a); }
 __device__ __forceinline__ double d_sqrt(double a) { return sqrt(a); }
 __device__ __forceinline__ float d_tanh(float a) { return tanhf(a); }
 __device__ __forceinline__ double d_tanh(double a) { return tanh(a); }
-__device__ __forceinline__ float d_pow(float a, float e) { return powf(a, e); }
-__device__ __forceinline__ double d_pow(double a, double e) {
-  return pow(a, e);
-}
 
 // Square-and-multiply for integer dtypes (reference: int_pow,
 // src/cpp/ops/unary_ops.cu:40-49).
@@ -47,6 +44,7 @@ template <class T> __device__ __forceinline__ T int_pow(T a, T n) {
 
 template <int OP, class T> struct UnaryFwd {
   T e; // exponent for NT_POW, as the reference's value.item<T>()
+  PowPlan plan;
   __device__ __forceinline__ void operator()(const T (&x)[1], T (&y)[1]) const {
     const T a = x[0];
     if constexpr (OP == NT_EXP)
@@ -67,7 +65,7 @@ template <int OP, class T> struct UnaryFwd {
       if constexpr (std::is_integral_v<T>)
         y[0] = int_pow(a, e);
       else
-        y[0] = d_pow(a, e);
+        y[0] = pow_planned(a, e, plan);
     }
   }
 };
@@ -114,7 +112,8 @@ namespace {
 
 template <int OP, class T> void run_unary(const nt_view *x, double scalar,
                                           const nt_view *out) {
-  UnaryFwd<OP, T> f{static_cast<T>(scalar)};
+  const T e = static_cast<T>(scalar);
+  UnaryFwd<OP, T> f{e, make_pow_plan(double(e))};
   const nt_view *ins[1] = {x};
   const nt_view *outs[1] = {out};
   launch_elementwise<T, T, 1, 1>(ins, outs, f);

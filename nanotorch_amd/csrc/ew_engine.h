@@ -31,6 +31,11 @@
 
 #include "nt_internal.h"
 
+// Vector groups per thread in the contiguous (flat) kernel.
+#ifndef NT_FLAT_UNROLL
+#define NT_FLAT_UNROLL 2
+#endif
+
 namespace nt {
 
 constexpr int EW_THREADS = 256;
@@ -522,7 +527,7 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
   if (flat) {
     constexpr int VBIG = ew_vec<TI>() < ew_vec<TO>() ? ew_vec<TI>()
                                                       : ew_vec<TO>();
-    constexpr int UNROLL = 2;
+    constexpr int UNROLL = NT_FLAT_UNROLL;
     bool aligned = true;
     for (int k = 0; k < NI; ++k)
       if (!(smask & (1u << k)) &&

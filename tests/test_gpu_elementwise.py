@@ -300,3 +300,64 @@ def test_config2_full_size(gpu, layout):
     assert_bitexact(host(tgt), O.accumulate(old, O.binary(O.MUL, b, g)), "mul bwd 2^24")
     got = host(nt.Tensor._new_contiguous(K.unary(_lib.TANH, xa), shape))
     assert_rel(got, O.unary(O.TANH, a), 1e-6, "tanh 2^24")
+
+
+# ------------------------------------------------- pow exponent fast paths
+
+POW_EXPONENTS = [0.0, -0.0, 1.0, 2.0, 3.0, 4.0, -1.0, -2.0, -3.0, -4.0, 0.5, 1.5,
+                 2.5, 3.5, 4.5, -0.5, -1.5, -2.5, -4.5, 5.0, 6.5, 1.25, -7.3]
+
+
+def _pow_inputs(dtype):
+    """Normal values over a wide range of both signs, then every special
+    class pow distinguishes: +-0, +-inf, NaN, subnormals, values whose
+    small powers overflow or underflow, and +-1."""
+    r = rng(seed_of("pow-special", np.dtype(dtype).name))
+    fi = np.finfo(dtype)
+    mags = np.exp(r.uniform(np.log(1e-6), np.log(1e6), 4000))
+    vals = np.concatenate([mags, -mags[:1000], r.uniform(0.1, 4, 1000)])
+    special = [0.0, -0.0, np.inf, -np.inf, np.nan, 1.0, -1.0, fi.tiny, -fi.tiny,
+               fi.tiny / 8, -fi.tiny / 8, fi.max, -fi.max, fi.max ** 0.25,
+               fi.max ** 0.3, fi.tiny ** 0.25, fi.tiny ** 0.2, 2.0, 0.5]
+    return np.concatenate([vals, np.array(special)]).astype(dtype)
+
+
+def _assert_pow_close(got, want, rel, what):
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn), f"{what}: NaN positions differ at {np.nonzero(gn != wn)[0][:5]}"
+    g, w = got[~gn].astype(np.float64), want[~wn].astype(np.float64)
+    inf = np.isinf(w) | np.isinf(g)
+    assert np.array_equal(g[inf], w[inf]), f"{what}: infinities differ"
+    g, w = g[~inf], w[~inf]
+    sub = float(np.finfo(got.dtype).smallest_subnormal)
+    err = np.abs(g - w)
+    bad = err > rel * np.abs(w) + 2 * sub
+    if bad.any():
+        i = int(np.argmax(np.where(bad, err / np.maximum(np.abs(w), 1e-300), 0)))
+        raise AssertionError(f"{what}: {int(bad.sum())} outside rel {rel}; "
+                             f"got {g[i]!r} want {w[i]!r}")
+    assert np.array_equal(np.signbit(g), np.signbit(w)), f"{what}: signs differ"
+
+
+@pytest.mark.parametrize("dtype,rel", [(np.float32, 1e-6), (np.float64, 1e-14)])
+@pytest.mark.parametrize("e", POW_EXPONENTS)
+def test_pow_exponent_classes(gpu, e, dtype, rel):
+    """Integer and half-integer exponents with |e| <= 4.5 take the
+    multiply/sqrt path, the rest the library pow; both must agree with the
+    host pow (glibc) on normal values and reproduce its special values."""
+    a = _pow_inputs(dtype)
+    got = host(nt.Tensor._new_contiguous(K.unary(_lib.POW, dev(a), e), a.shape))
+    want = O.unary(O.POW, a, e) if dtype == np.float32 else np.power(a, dtype(e))
+    _assert_pow_close(got, want, rel, f"pow e={e} {np.dtype(dtype).name}")
+
+
+@pytest.mark.parametrize("e", [2.0, 3.0, 1.5, 0.5, -1.0, -0.5, 4.5, 1.0])
+def test_pow_backward_exponent_classes(gpu, e):
+    """Backward evaluates pow(x, e - 1): the exponents above land on each
+    fast-path class (and e = 1 on x**0)."""
+    a = _pow_inputs(np.float32)
+    g = rng(seed_of("pow-bwd", e)).standard_normal(a.shape).astype(np.float32)
+    want = O.bwd_pow(g, a, e)
+    got = host(nt.Tensor._new_contiguous(K.unary_bwd(_lib.POW, dev(g), dev(a), e, None),
+                                         a.shape))
+    _assert_pow_close(got, want, 1e-6, f"pow bwd e={e}")
