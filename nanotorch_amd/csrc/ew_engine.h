@@ -162,6 +162,77 @@ __global__ __launch_bounds__(EW_THREADS) void ew_flat_kernel(
   }
 }
 
+// ------------------------------------------------------------------- rows
+
+// Row-major [R, C] outputs whose inputs are each a full [R, C] operand, a
+// broadcast row (strides 0, 1: a bias), a broadcast column (strides s, 0:
+// a reduced axis re-expanded) or a scalar.  Work-items take VEC-wide groups
+// along the rows as in the flat kernel; the group's (r, c) comes from one
+// multiply-high division by C (C % VEC == 0, so a group never straddles two
+// rows).  Broadcast rows are re-read by every row of the grid and stay in
+// cache, so they are loaded without the streaming hint.
+template <class TI, class TO, int NI, int NO, int VEC, int UNROLL, bool NTL,
+          class F>
+__global__ __launch_bounds__(EW_THREADS) void ew_rows_kernel(
+    PtrPack<const TI, NI> in, uint32_t scalar_mask, uint32_t rowb_mask,
+    uint32_t colb_mask, Strides2<NI> sin, PtrPack<TO, NO> out, uint32_t nvec,
+    FastDivU32 fdc, uint32_t C, F f) {
+  using VI = VecT<TI, VEC>;
+  using VO = VecT<TO, VEC>;
+  const uint32_t base = blockIdx.x * (EW_THREADS * UNROLL) + threadIdx.x;
+  VI a[UNROLL][NI > 0 ? NI : 1];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const uint32_t vi = base + uint32_t(u) * EW_THREADS;
+    if (vi < nvec) {
+      const uint32_t i = vi * VEC;
+      const uint32_t r = fdc.div(i);
+      const uint32_t c = i - r * C;
+#pragma unroll
+      for (int k = 0; k < NI; ++k) {
+        const uint32_t bit = 1u << k;
+        if (scalar_mask & bit) {
+          const TI v = in.p[k][0];
+#pragma unroll
+          for (int j = 0; j < VEC; ++j)
+            a[u][k].v[j] = v;
+        } else if (colb_mask & bit) {
+          const TI v = in.p[k][int64_t(r) * sin.r[k]];
+#pragma unroll
+          for (int j = 0; j < VEC; ++j)
+            a[u][k].v[j] = v;
+        } else if (rowb_mask & bit) {
+          a[u][k] = vload<false, TI, VEC>(in.p[k] + c);
+        } else {
+          a[u][k] = vload<NTL, TI, VEC>(in.p[k] + i);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const uint32_t vi = base + uint32_t(u) * EW_THREADS;
+    if (vi < nvec) {
+      VO o[NO];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        TI x[NI > 0 ? NI : 1];
+        TO y[NO];
+#pragma unroll
+        for (int k = 0; k < NI; ++k)
+          x[k] = a[u][k].v[j];
+        f(x, y);
+#pragma unroll
+        for (int m = 0; m < NO; ++m)
+          o[m].v[j] = y[m];
+      }
+#pragma unroll
+      for (int m = 0; m < NO; ++m)
+        reinterpret_cast<VO *>(out.p[m])[vi] = o[m];
+    }
+  }
+}
+
 // --------------------------------------------------------------- tile2d x4
 
 // 64x64 tile with 4-element vector accesses (16 B for fp32).  Work-item t
@@ -551,6 +622,54 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
           <<<grid, EW_THREADS, 0, s>>>(pin, smask, pout, n, n, f);
     NT_LAUNCH_CHECK();
     return;
+  }
+
+  // ---- rows: contiguous [R, C] outputs, inputs full / broadcast / scalar.
+  if (L.ndim == 2) {
+    constexpr int VBIG = ew_vec<TI>() < ew_vec<TO>() ? ew_vec<TI>()
+                                                      : ew_vec<TO>();
+    const int64_t R = L.shape[0], C = L.shape[1];
+    bool rows = C % VBIG == 0 && n < (int64_t(1) << 32);
+    uint32_t sm = 0, rb = 0, cb = 0;
+    Strides2<NI> sin{};
+    for (int m = 0; m < NO && rows; ++m)
+      rows = L.strides[NI + m][0] == C && L.strides[NI + m][1] == 1 &&
+             reinterpret_cast<uintptr_t>(pout.p[m]) % (sizeof(TO) * VBIG) == 0;
+    for (int k = 0; k < NI && rows; ++k) {
+      const int64_t sr = L.strides[k][0], sc = L.strides[k][1];
+      sin.r[k] = sr;
+      sin.c[k] = sc;
+      const bool al =
+          reinterpret_cast<uintptr_t>(pin.p[k]) % (sizeof(TI) * VBIG) == 0;
+      if (sr == 0 && sc == 0)
+        sm |= 1u << k;
+      else if (sc == 0)
+        cb |= 1u << k;
+      else if (sr == 0 && sc == 1 && al)
+        rb |= 1u << k;
+      else if (!(sr == C && sc == 1 && al))
+        rows = false;
+    }
+    // Worth it only when something is broadcast (otherwise the operands
+    // would have coalesced to the flat case).
+    if (rows && (rb | cb) != 0 && R > 0) {
+      constexpr int UNROLL = NT_FLAT_UNROLL;
+      const int64_t nvec = n / VBIG;
+      const int64_t blocks = std::max<int64_t>(
+          1, (nvec + EW_THREADS * UNROLL - 1) / (EW_THREADS * UNROLL));
+      const dim3 grid{unsigned(blocks), 1u, 1u};
+      const FastDivU32 fdc{uint32_t(C)};
+      if (ntl)
+        ew_rows_kernel<TI, TO, NI, NO, VBIG, UNROLL, true, F>
+            <<<grid, EW_THREADS, 0, s>>>(pin, sm, rb, cb, sin, pout,
+                                         uint32_t(nvec), fdc, uint32_t(C), f);
+      else
+        ew_rows_kernel<TI, TO, NI, NO, VBIG, UNROLL, false, F>
+            <<<grid, EW_THREADS, 0, s>>>(pin, sm, rb, cb, sin, pout,
+                                         uint32_t(nvec), fdc, uint32_t(C), f);
+      NT_LAUNCH_CHECK();
+      return;
+    }
   }
 
   // ---- tile2d

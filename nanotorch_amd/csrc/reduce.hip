@@ -70,11 +70,16 @@ template <class O, bool IS_MAX> struct SelAcc {
     else
       return a < b;
   }
-  // Branch-free update (selects, no divergent control flow).
+  // Branch-free update (selects, no divergent control flow).  Every kernel
+  // feeds an accumulator its elements in increasing j, so on a tie the
+  // stored, earlier index stays -- unless nothing equal has been counted yet
+  // (c == 0: the neutral value with index INT64_MAX met an element equal to
+  // it), when the element's index is the first.
   __device__ __forceinline__ void add(O x, int64_t jj) {
     const bool b = better(x, v);
     const bool e = (x == v);
-    j = b ? jj : ((e && jj < j) ? jj : j);
+    const bool take = b || (e && c == 0);
+    j = take ? jj : j;
     c = b ? 1 : c + (e ? 1 : 0);
     v = b ? x : v;
   }
@@ -219,16 +224,24 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
 }
 
 // x is [D, K] with K contiguous (stride 1) and row stride sd.  Block
-// (bx, s): columns [bx*64*VEC, +64*VEC), rows [s*seg, ..).  Lane l owns VEC
-// adjacent columns; wave w walks rows w, w+4, ...
-template <class T, class O, class Acc, int VEC, int MODE>
+// (bx, s) covers columns [bx * CB, +CB), CB = 64 * VEC * WC, and rows
+// [s * seg, ..): WC waves stand side by side (lane l owns VEC adjacent
+// columns, so a block reads CB * sizeof(T) contiguous bytes of each row) and
+// the RED_WAVES / WC wave rows interleave the segment's rows, UR rows in
+// flight per lane.  Partials go to partial[s * K + k] (coalesced), combined
+// by reduce_col_combine_kernel.
+template <class T, class O, class Acc, int VEC, int WC, int UR, int MODE>
 __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
     const T *__restrict__ x, int64_t K, int64_t D, int64_t sd, int64_t seg,
     int S, Acc *partial, RedOut<MODE> out) {
-  __shared__ Acc lds[RED_WAVES][64 * VEC];
+  constexpr int WR = RED_WAVES / WC;
+  constexpr int CB = 64 * VEC * WC;
+  __shared__ Acc lds[WR > 1 ? RED_WAVES : 1][64 * VEC];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wc = w % WC, wr = w / WC;
   const int s = blockIdx.y;
-  const int64_t k0 = int64_t(blockIdx.x) * 64 * VEC + int64_t(lane) * VEC;
+  const int64_t k0 =
+      int64_t(blockIdx.x) * CB + int64_t(wc) * 64 * VEC + int64_t(lane) * VEC;
   const int64_t j0 = int64_t(s) * seg;
   const int64_t j1 = j0 + seg < D ? j0 + seg : D;
   Acc a[VEC];
@@ -237,51 +250,92 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
     a[i].init();
   using V = VecT<T, VEC>;
   if (k0 + VEC <= K) {
-    // Four rows in flight per work-item, then the tail.
-    constexpr int UR = 4;
-    int64_t j = j0 + w;
-    for (; j + (UR - 1) * RED_WAVES < j1; j += UR * RED_WAVES) {
+    int64_t j = j0 + wr;
+    for (; j + (UR - 1) * WR < j1; j += UR * WR) {
       V v[UR];
 #pragma unroll
       for (int u = 0; u < UR; ++u)
-        v[u] = vload<true, T, VEC>(x + (j + u * RED_WAVES) * sd + k0);
+        v[u] = vload<true, T, VEC>(x + (j + u * WR) * sd + k0);
 #pragma unroll
       for (int u = 0; u < UR; ++u)
 #pragma unroll
         for (int i = 0; i < VEC; ++i)
-          a[i].add(static_cast<O>(v[u].v[i]), j + u * RED_WAVES);
+          a[i].add(static_cast<O>(v[u].v[i]), j + u * WR);
     }
-    for (; j < j1; j += RED_WAVES) {
+    for (; j < j1; j += WR) {
       const V v = vload<true, T, VEC>(x + j * sd + k0);
 #pragma unroll
       for (int i = 0; i < VEC; ++i)
         a[i].add(static_cast<O>(v.v[i]), j);
     }
-  } else {
-    for (int64_t j = j0 + w; j < j1; j += RED_WAVES)
+  } else if (k0 < K) {
+    for (int64_t j = j0 + wr; j < j1; j += WR)
       for (int i = 0; i < VEC; ++i)
         if (k0 + i < K)
           a[i].add(static_cast<O>(x[j * sd + k0 + i]), j);
   }
+  if constexpr (WR > 1) {
+    // Wave rows of one column group merge in wave-row order.
 #pragma unroll
-  for (int i = 0; i < VEC; ++i)
-    lds[w][lane * VEC + i] = a[i];
-  __syncthreads();
-  if (w == 0) {
+    for (int i = 0; i < VEC; ++i)
+      lds[w][lane * VEC + i] = a[i];
+    __syncthreads();
+    if (wr == 0) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+#pragma unroll
+        for (int rr = 1; rr < WR; ++rr)
+          a[i].merge(lds[rr * WC + wc][lane * VEC + i]);
+    }
+  }
+  if (wr == 0) {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      Acc r = lds[0][lane * VEC + i];
-#pragma unroll
-      for (int ww = 1; ww < RED_WAVES; ++ww)
-        r.merge(lds[ww][lane * VEC + i]);
       const int64_t k = k0 + i;
       if (k < K) {
         if (S == 1)
-          out.template write<O>(k, r);
+          out.template write<O>(k, a[i]);
         else
-          partial[k * S + s] = r;
+          partial[int64_t(s) * K + k] = a[i];
       }
     }
+  }
+}
+
+// Combines partial[s * K + k] over s for 64 columns per block: wave w
+// merges s = w, w + 4, ... (UR loads in flight), then the four waves merge
+// in order through LDS.
+template <class O, class Acc, int MODE>
+__global__ __launch_bounds__(RED_THREADS) void reduce_col_combine_kernel(
+    const Acc *__restrict__ partial, int64_t K, int S, RedOut<MODE> out) {
+  constexpr int UR = 4;
+  __shared__ Acc lds[RED_WAVES][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t k = int64_t(blockIdx.x) * 64 + lane;
+  Acc a;
+  a.init();
+  if (k < K) {
+    int s = w;
+    for (; s + RED_WAVES * (UR - 1) < S; s += RED_WAVES * UR) {
+      Acc t[UR];
+#pragma unroll
+      for (int u = 0; u < UR; ++u)
+        t[u] = partial[int64_t(s + RED_WAVES * u) * K + k];
+#pragma unroll
+      for (int u = 0; u < UR; ++u)
+        a.merge(t[u]);
+    }
+    for (; s < S; s += RED_WAVES)
+      a.merge(partial[int64_t(s) * K + k]);
+  }
+  lds[w][lane] = a;
+  __syncthreads();
+  if (w == 0 && k < K) {
+    Acc r = lds[0][lane];
+#pragma unroll
+    for (int i = 1; i < RED_WAVES; ++i)
+      r.merge(lds[i][lane]);
+    out.template write<O>(k, r);
   }
 }
 
@@ -327,17 +381,29 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_generic_kernel(
 
 // Combines the S partials of slice k (one wave per slice), in segment order
 // per lane, then across lanes.
-template <class O, class Acc, int MODE>
-__global__ __launch_bounds__(64) void reduce_combine_kernel(
+// Combines partial[k * S + s] over s, one workgroup of NT work-items per
+// slice k: item t merges s = t, t + NT, ..., then the waves merge in order.
+template <class O, class Acc, int MODE, int NT>
+__global__ __launch_bounds__(NT) void reduce_combine_kernel(
     const Acc *__restrict__ partial, int S, RedOut<MODE> out) {
+  __shared__ Acc lds[NT / 64];
   const int64_t k = blockIdx.x;
   Acc a;
   a.init();
-  for (int s = threadIdx.x; s < S; s += 64)
+  for (int s = threadIdx.x; s < S; s += NT)
     a.merge(partial[k * S + s]);
   wave_reduce(a);
-  if (threadIdx.x == 0)
-    out.template write<O>(k, a);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0)
+    lds[w] = a;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Acc r = lds[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i)
+      r.merge(lds[i]);
+    out.template write<O>(k, r);
+  }
 }
 
 // ------------------------------------------------------------------- plan
@@ -418,10 +484,16 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
   constexpr bool FAST = std::is_same_v<T, O> &&
                         (std::is_same_v<T, float> || std::is_same_v<T, double>);
 
+  // Second pass over partial[k * S + s]: few slices get 1024 work-items
+  // each (a full reduction's S partials in two loads per item).
   auto finish = [&](Acc *partial, int S) {
     if (S > 1) {
-      reduce_combine_kernel<O, Acc, MODE>
-          <<<dim3(unsigned(p.K)), 64, 0, st>>>(partial, S, out);
+      if (p.K <= 64)
+        reduce_combine_kernel<O, Acc, MODE, 1024>
+            <<<dim3(unsigned(p.K)), 1024, 0, st>>>(partial, S, out);
+      else
+        reduce_combine_kernel<O, Acc, MODE, RED_THREADS>
+            <<<dim3(unsigned(p.K)), RED_THREADS, 0, st>>>(partial, S, out);
       NT_LAUNCH_CHECK();
     }
     if (partial)
@@ -439,9 +511,11 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
     for (int d = 0; d < p.keep.ndim; ++d)
       if (p.keep.strides[d] % VEC != 0)
         aligned = false;
+    // Long slices are split so that about 4 workgroups per CU stream.
+    const int64_t row_target = int64_t(device_cu_count()) * 4;
     int64_t S = 1;
-    if (p.K < target_blocks)
-      S = std::min<int64_t>(ceil_div(target_blocks, p.K),
+    if (p.K < row_target)
+      S = std::min<int64_t>(ceil_div(row_target, p.K),
                             std::max<int64_t>(1, p.D / (RED_THREADS * 16)));
     S = std::max<int64_t>(1, std::min<int64_t>(S, 1 << 16));
     int64_t seg = ceil_div(p.D, S);
@@ -474,9 +548,18 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
         reinterpret_cast<uintptr_t>(xp) % (sizeof(T) * VEC) == 0 &&
         sd % VEC == 0;
     const int vec = aligned ? VEC : 1;
-    const int64_t bx = ceil_div(K, 64 * vec);
-    int64_t S = std::max<int64_t>(1, ceil_div(target_blocks, bx));
-    S = std::min<int64_t>(S, std::max<int64_t>(1, D / (RED_WAVES * 8)));
+    // Wide tensors: 4 waves side by side (64 * vec * 4 columns per
+    // workgroup); narrow ones: 1 column group, 4 wave rows.
+    constexpr int UR = 8;
+    const int wc = K >= 4 * 64 * vec ? 4 : 1;
+    const int64_t bx = ceil_div(K, int64_t(64) * vec * wc);
+    // About one (sum) or two (max/min, larger partials) workgroups per CU:
+    // fewer, longer row walks with UR loads in flight measured faster than
+    // many short ones, and keep the partials small.
+    const int64_t col_target =
+        int64_t(device_cu_count()) * (sizeof(Acc) <= 8 ? 1 : 2);
+    int64_t S = std::max<int64_t>(1, ceil_div(col_target, bx));
+    S = std::min<int64_t>(S, std::max<int64_t>(1, D / (UR * (RED_WAVES / wc))));
     S = std::min<int64_t>(S, 65535);
     const int64_t seg = ceil_div(D, S);
     S = ceil_div(D, seg);
@@ -486,14 +569,27 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
     if (bx >= (int64_t(1) << 31))
       fail(NT_ERR_RUNTIME, "reduction too large");
     const dim3 grid{unsigned(bx), unsigned(S), 1u};
-    if (aligned)
-      reduce_col_kernel<T, O, Acc, VEC, MODE><<<grid, RED_THREADS, 0, st>>>(
-          xp, K, D, sd, seg, int(S), partial, out);
+    if (aligned && wc == 4)
+      reduce_col_kernel<T, O, Acc, VEC, 4, UR, MODE>
+          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
+    else if (aligned)
+      reduce_col_kernel<T, O, Acc, VEC, 1, UR, MODE>
+          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
+    else if (wc == 4)
+      reduce_col_kernel<T, O, Acc, 1, 4, UR, MODE>
+          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
     else
-      reduce_col_kernel<T, O, Acc, 1, MODE><<<grid, RED_THREADS, 0, st>>>(
-          xp, K, D, sd, seg, int(S), partial, out);
+      reduce_col_kernel<T, O, Acc, 1, 1, UR, MODE>
+          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
     NT_LAUNCH_CHECK();
-    finish(partial, int(S));
+    if (S > 1) {
+      reduce_col_combine_kernel<O, Acc, MODE>
+          <<<dim3(unsigned(ceil_div(K, 64))), RED_THREADS, 0, st>>>(
+              partial, K, int(S), out);
+      NT_LAUNCH_CHECK();
+    }
+    if (partial)
+      device_free(partial);
     return;
   }
 

@@ -161,6 +161,37 @@ def test_broadcast_and_strided_views(gpu):
     assert_bitexact(got, O.unary(O.RELU, np.ascontiguousarray(a.transpose(2, 1, 0))), "3d-T")
 
 
+@pytest.mark.parametrize("shape", [(64, 1024), (3, 8), (129, 4096), (2, 3, 16)])
+def test_broadcast_rows(gpu, shape):
+    """Contiguous operands with a broadcast row (bias), a broadcast column,
+    and a scalar, in every operand position; plus an unaligned variant."""
+    r = rng(seed_of("rows", shape))
+    a = r.standard_normal(shape).astype(np.float32)
+    row = r.uniform(0.5, 2, shape[-1:]).astype(np.float32)
+    colshape = shape[:-1] + (1,)
+    col = r.uniform(0.5, 2, colshape).astype(np.float32)
+    sc = np.array(1.75, dtype=np.float32)
+    cases = [
+        (dev(row).expand(*shape), np.broadcast_to(row, shape)),
+        (dev(col).expand(*shape), np.broadcast_to(col, shape)),
+        (dev(sc.reshape((1,) * len(shape))).expand(*shape), np.broadcast_to(sc, shape)),
+    ]
+    x = dev(a)
+    for op, oop in ((_lib.ADD, O.ADD), (_lib.SUB, O.SUB), (_lib.MUL, O.MUL), (_lib.DIV, O.DIV)):
+        for other, onp in cases:
+            onp = np.ascontiguousarray(onp)
+            got = host(nt.Tensor._new_contiguous(K.binary(op, x, other), shape))
+            assert_bitexact(got, O.binary(oop, a, onp), f"op {op} bcast right")
+            got = host(nt.Tensor._new_contiguous(K.binary(op, other, x), shape))
+            assert_bitexact(got, O.binary(oop, onp, a), f"op {op} bcast left")
+    # unaligned base pointer (one-element offset) takes another path
+    big = r.standard_normal((int(np.prod(shape)) + 1,)).astype(np.float32)
+    xu = dev(big)[1:].reshape(*shape)
+    got = host(nt.Tensor._new_contiguous(K.binary(_lib.MUL, xu, cases[0][0]), shape))
+    want = O.binary(O.MUL, big[1:].reshape(shape), np.ascontiguousarray(cases[0][1]))
+    assert_bitexact(got, want, "unaligned")
+
+
 @pytest.mark.parametrize("src,dst", [(np.float32, np.float64), (np.float64, np.float32),
                                      (np.float32, np.int64), (np.int64, np.float32),
                                      (np.float32, np.bool_), (np.bool_, np.float32),

@@ -31,6 +31,9 @@ SHAPES_AXES = [
     ((1000, 257), (0,)),
     ((64, 4096), (1,)),
     ((4096, 64), (0,)),
+    ((300, 2050), (0,)),
+    ((513, 4096), (0,)),
+    ((33, 1030), (0,)),
     ((10, 2, 5, 1), (1, 3)),
     ((10, 2, 5, 1), (3, 1)),
     ((7, 9, 11), (0, 2)),
