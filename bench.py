@@ -18,6 +18,11 @@ workload.
 
 Data is synthetic (seeded normal / uniform per config); weights of the MLP
 are random He-normal.
+
+Profiles: `python bench.py --summarize KIND DIR [DIR2]` turns the csv output
+of the rocprofv3 commands in PROFILE_CMDS into the summaries kept under
+profiles/ (kernel statistics per part, and HBM bytes per launch from the
+FETCH_SIZE / WRITE_SIZE passes, which the roofline's `traffic` reads).
 """
 
 from __future__ import annotations
@@ -378,6 +383,109 @@ def cpu_baseline(rows: int = 1024) -> dict:
             "host_cpu": cpu, "host_nproc": os.cpu_count()}
 
 
+# ---------------------------------------------------------------- profiles
+
+_PROF = "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/{d} -o run -- python -u bench.py {a}"
+_PMC = "rocprofv3 --pmc {c} --output-format csv -d gpurun_out/{d} -o run -- python -u bench.py {a}"
+PROFILE_CMDS = {
+    "sweep": _PROF.format(d="prof_sweep", a="--steps 5 --warmup 2 --parts ew --calib"),
+    "red": _PROF.format(d="prof_red", a="--parts red"),
+    "mm": _PROF.format(d="prof_mm", a="--parts mm"),
+    "mlp": _PROF.format(d="prof_mlp", a="--parts mlp --mlp-steps 5"),
+    "fetch": _PMC.format(c="FETCH_SIZE", d="prof_fetch", a="--steps 1 --warmup 0 --parts ew --calib"),
+    "write": _PMC.format(c="WRITE_SIZE", d="prof_write", a="--steps 1 --warmup 0 --parts ew --calib"),
+}
+PROFILE_FILES = {
+    "sweep": ("elementwise_sweep_config2_trace.md", "Kernel statistics: config-2 elementwise sweep (the headline)"),
+    "red": ("reduce_config3_trace.md", "Kernel statistics: config-3 reductions [8192, 8192] fp32"),
+    "mm": ("matmul_config4_trace.md", "Kernel statistics: config-4 MatMulOp forward + dA + dB"),
+    "mlp": ("mlp_config5_trace.md", "Kernel statistics: config-5 4-layer MLP training steps"),
+}
+_UN = {0: "exp", 1: "log", 2: "neg", 3: "relu", 4: "sqrt", 5: "tanh", 6: "sigmoid", 7: "pow"}
+_BI = {0: "add", 1: "sub", 2: "mul", 3: "truediv"}
+
+
+def _short(name: str) -> str:
+    import re
+    n = re.sub(r"\(.*$", "", name)
+    return n.replace("void nt::", "").replace("nt::", "").replace("(anonymous namespace)::", "")
+
+
+def _sweep_key(name: str):
+    """Kernel name -> 'op|layout|phase' of the sweep (flat kernel: contiguous
+    operands; tile kernel: transposed views)."""
+    import re
+    layout = "contig" if "ew_flat_kernel" in name else ("transposed" if "ew_tile4_kernel" in name else None)
+    m = re.search(r"(UnaryFwd|UnaryBwd|BinaryFwd|BinaryBwd)<(\d+)", name)
+    if not layout or not m:
+        return None
+    kind, op = m.group(1), int(m.group(2))
+    opn = (_UN if kind.startswith("Unary") else _BI)[op]
+    return f"{opn}|{layout}|{'fwd' if kind.endswith('Fwd') else 'bwd'}"
+
+
+def summarize(kind: str, dirs: list[str]) -> None:
+    import csv
+    prof = os.path.join(ROOT, "profiles")
+    if kind in PROFILE_FILES:
+        fname, title = PROFILE_FILES[kind]
+        rows = list(csv.DictReader(open(os.path.join(dirs[0], "run_kernel_stats.csv"))))
+        o = [f"# {title}\n", "Command (repo root on the GPU box):\n",
+             f"```\n{PROFILE_CMDS[kind]}\n```\n",
+             f"Summarised with `python bench.py --summarize {kind} gpurun_out/prof_{kind}`.",
+             "Durations are rocprofv3 kernel times in microseconds; a sweep row's",
+             "`sweep key` names the bench.py entry it belongs to.\n",
+             "| kernel | sweep key | calls | avg us | min us | max us | total % |",
+             "|---|---|---|---|---|---|---|"]
+        for r in rows:
+            o.append(f"| `{_short(r['Name'])[:150]}` | {_sweep_key(r['Name']) or ''} | {r['Calls']} | "
+                     f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                     f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+        with open(os.path.join(prof, fname), "w") as f:
+            f.write("\n".join(o) + "\n")
+        return
+    if kind != "traffic":
+        raise SystemExit(f"unknown profile kind {kind}")
+
+    def load(path, counter):
+        d: dict[str, list[float]] = {}
+        for r in csv.DictReader(open(os.path.join(path, "run_counter_collection.csv"))):
+            if r.get("Counter_Name") == counter:
+                d.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in d.items()}
+
+    fch, wr = load(dirs[0], "FETCH_SIZE"), load(dirs[1], "WRITE_SIZE")
+    copy = [k for k in fch if "CastOp<float, float>" in k][0]  # the --calib copies
+    fs = 64 * 1024 / fch[copy]  # counters are KiB; the copy reads 64 MiB
+    ws = 64 * 1024 / wr[copy]  # and writes 64 MiB
+    per, rows = {}, []
+    for k in fch:
+        kk = _sweep_key(k)
+        if kk is None:
+            continue
+        b = fch[k] * fs * 1024 + wr.get(k, 0) * ws * 1024
+        per[kk] = int(round(b))
+        rows.append((kk, fch[k] / 1024, wr.get(k, 0) / 1024, b / 2**20, ew_bytes(*kk.split("|")[::2]) / 2**20))
+    with open(os.path.join(prof, "traffic.json"), "w") as f:
+        json.dump({"source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on bench.py --calib, "
+                             "scaled by a plain copy's reading",
+                   "commands": [PROFILE_CMDS["fetch"], PROFILE_CMDS["write"]],
+                   "fetch_scale": fs, "write_scale": ws, "per_launch_bytes": per}, f, indent=1)
+    with open(os.path.join(prof, "elementwise_sweep_config2_hbm_traffic.md"), "w") as o:
+        o.write("# HBM traffic per launch: config-2 sweep kernels\n\n")
+        o.write(f"Commands (repo root on the GPU box):\n\n```\n{PROFILE_CMDS['fetch']}\n"
+                f"{PROFILE_CMDS['write']}\n```\n\n")
+        o.write("Summarised with `python bench.py --summarize traffic gpurun_out/prof_fetch "
+                "gpurun_out/prof_write` (also writes traffic.json, read by the roofline).\n\n")
+        o.write(f"Calibration: a plain copy of 2^24 fp32 (64 MiB read, 64 MiB written) reads "
+                f"FETCH_SIZE {fch[copy] / 1024:.1f} MiB and WRITE_SIZE {wr[copy] / 1024:.1f} MiB per "
+                f"dispatch, so FETCH_SIZE is scaled by {fs:.3f} and WRITE_SIZE by {ws:.3f}.\n\n")
+        o.write("| kernel | FETCH_SIZE MiB | WRITE_SIZE MiB | scaled traffic MiB | algorithmic MiB |\n"
+                "|---|---|---|---|---|\n")
+        for kk, fv, wv, t, alg in sorted(rows):
+            o.write(f"| {kk} | {fv:.1f} | {wv:.1f} | {t:.1f} | {alg:.1f} |\n")
+
+
 # -------------------------------------------------------------------- main
 
 
@@ -386,12 +494,19 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--parts", default="all", help="all | none | comma list of red,mm,mlp,cpu")
+    ap.add_argument("--parts", default="all",
+                    help="all | none (the headline sweep only) | comma list of ew,red,mm,mlp,cpu")
     ap.add_argument("--mlp-steps", type=int, default=20)
     ap.add_argument("--calib", action="store_true",
                     help="first run 3 plain copies of 2^24 fp32 (64 MiB read + 64 MiB "
                          "written each): the reference dispatch for HBM byte counters")
+    ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
+                    help="write a profiles/ summary from rocprofv3 csv output: "
+                         "sweep|red|mm|mlp DIR, or traffic FETCH_DIR WRITE_DIR")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize[0], args.summarize[1:])
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for {max(args.gpus, world)}); "
@@ -400,8 +515,8 @@ def main() -> int:
     if not nt.is_available():
         print("no HIP device / libnt.so", file=sys.stderr)
         return 1
-    parts = {"red", "mm", "mlp", "cpu"} if args.parts == "all" else (
-        set() if args.parts == "none" else set(args.parts.split(",")))
+    parts = {"ew", "red", "mm", "mlp", "cpu"} if args.parts == "all" else (
+        {"ew"} if args.parts == "none" else set(args.parts.split(",")))
 
     if args.calib:
         src = _fresh((N_ELEM,))
@@ -409,6 +524,18 @@ def main() -> int:
         for _ in range(3):
             K.copy_view(src, dst)
         nt.sync()
+
+    if "ew" not in parts:
+        # profiling runs of one part: print that part's results only
+        line = {"parts": {}}
+        if "red" in parts:
+            line["parts"]["reductions"] = bench_reductions()
+        if "mm" in parts:
+            line["parts"]["matmul"] = bench_matmul()
+        if "mlp" in parts:
+            line["parts"]["mlp"] = bench_mlp(args.mlp_steps)
+        print(json.dumps(line), flush=True)
+        return 0
 
     ew = bench_elementwise(args.steps, args.warmup)
     value = ew["step_bytes"] / (ew["ms_per_step"] * 1e-3) / 1e9
