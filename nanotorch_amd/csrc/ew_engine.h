@@ -1,15 +1,20 @@
 // Elementwise engine: one launcher that runs a device functor over NI input
-// and NO output views of one logical shape, picking among three kernels:
+// and NO output views of one logical shape, picking among four kernels:
 //
 //  * flat    -- every operand is contiguous in the same logical order (or a
 //               broadcast scalar).  Each thread moves UNROLL vectors of 16 B
-//               per operand (dwordx4 loads/stores, nontemporal loads).
+//               per operand (dwordx4 loads/stores with the streaming hint).
+//  * rows    -- 2-D, contiguous outputs, every input either contiguous, a
+//               broadcast row, a broadcast column or a scalar: flat-kernel
+//               I/O with the (row, column) of each vector from one
+//               multiply-high division.
 //  * tile2d  -- after merging dims, the iteration space is 2-D.  A 64x64 tile
 //               per workgroup; operands whose rows are contiguous are read
 //               straight; operands contiguous along the other axis (e.g.
 //               `x.T`) are staged through a padded LDS tile so both the
 //               global read and the global write stay coalesced.  Outputs
-//               laid out that way go back through the same LDS tile.  With
+//               laid out that way go back through the same LDS tile.  The
+//               tile walks whichever orientation exchanges less.  With
 //               4-aligned sizes and strides every access is a 16-byte vector
 //               (ew_tile4_kernel); otherwise element accesses
 //               (ew_tile_kernel).
@@ -697,6 +702,28 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
 
   // ---- tile2d
   if (L.ndim == 2) {
+    // Elements are independent, so the tile may walk the transposed index
+    // space.  Column-major operands go through the LDS exchange; pick the
+    // orientation in which that costs less, an exchanged output counting
+    // as three exchanged inputs (measured: two `.T` inputs and a row-major
+    // output beat two row-major inputs and a `.T` output).  E.g. a backward
+    // whose saved tensors and gradients are `.T` views exchanges only the
+    // upstream gradient instead of four inputs and two outputs.
+    constexpr int OUT_COST = 3;
+    int cost_keep = 0, cost_swap = 0;
+    for (int k = 0; k < NT; ++k) {
+      const int64_t sr = L.strides[k][0], sc = L.strides[k][1];
+      const int wgt = k < NI ? 1 : OUT_COST;
+      if (sc == 1 && sr != 0) // row-major now, exchanged after a swap
+        cost_swap += wgt;
+      else if (sr == 1 && sc != 0) // column-major now
+        cost_keep += wgt;
+    }
+    if (cost_swap < cost_keep) {
+      std::swap(L.shape[0], L.shape[1]);
+      for (int k = 0; k < NT; ++k)
+        std::swap(L.strides[k][0], L.strides[k][1]);
+    }
     Strides2<NI> sin{};
     Strides2<NO> sout{};
     uint32_t col_in = 0, col_out = 0, row_in = 0, row_out = 0, bcol_in = 0;

@@ -105,6 +105,47 @@ template <class O, bool IS_MAX> struct SelAcc {
   }
 };
 
+// Accumulators used inside a column walk (reduce_col_kernel).  Sums use
+// SumAcc itself.  Max/min keep the index as a 32-bit offset from the
+// segment's first row -- the row is wave-uniform there, so the fold selects
+// one 32-bit register instead of a 64-bit pair -- and widen it once at the
+// end.  The update rule is SelAcc::add's.
+template <class O, bool IS_MAX> struct SelAcc32 {
+  O v;
+  int32_t j;
+  int32_t c;
+  __device__ __forceinline__ void init() {
+    v = IS_MAX ? std::numeric_limits<O>::lowest()
+               : std::numeric_limits<O>::max();
+    j = 0;
+    c = 0;
+  }
+  __device__ __forceinline__ void add(O x, int32_t jj) {
+    const bool b = SelAcc<O, IS_MAX>::better(x, v);
+    const bool e = (x == v);
+    const bool take = b || (e && c == 0);
+    j = take ? jj : j;
+    c = b ? 1 : c + (e ? 1 : 0);
+    v = b ? x : v;
+  }
+};
+
+template <class Acc> struct ColLocal {
+  using type = Acc;
+  __device__ static Acc widen(const Acc &a, int64_t) { return a; }
+};
+template <class O, bool IS_MAX> struct ColLocal<SelAcc<O, IS_MAX>> {
+  using type = SelAcc32<O, IS_MAX>;
+  __device__ static SelAcc<O, IS_MAX> widen(const type &a, int64_t j0) {
+    SelAcc<O, IS_MAX> r;
+    r.v = a.v;
+    // c == 0: no element was taken, the index stays the neutral INT64_MAX
+    r.j = a.c == 0 ? std::numeric_limits<int64_t>::max() : j0 + a.j;
+    r.c = a.c;
+    return r;
+  }
+};
+
 // Writes the final accumulator of slice k.
 // MODE 0: sum value; 1: extremum value (+ optional idx/count); 2: index.
 template <int MODE> struct RedOut {
@@ -243,37 +284,44 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
   const int64_t k0 =
       int64_t(blockIdx.x) * CB + int64_t(wc) * 64 * VEC + int64_t(lane) * VEC;
   const int64_t j0 = int64_t(s) * seg;
-  const int64_t j1 = j0 + seg < D ? j0 + seg : D;
-  Acc a[VEC];
+  // rows of this segment, relative to j0 (seg < 2^31, checked by the host)
+  const int32_t nr = int32_t((j0 + seg < D ? j0 + seg : D) - j0);
+  const T *base = x + j0 * sd + k0;
+  using LA = typename ColLocal<Acc>::type;
+  LA la[VEC];
 #pragma unroll
   for (int i = 0; i < VEC; ++i)
-    a[i].init();
+    la[i].init();
   using V = VecT<T, VEC>;
   if (k0 + VEC <= K) {
-    int64_t j = j0 + wr;
-    for (; j + (UR - 1) * WR < j1; j += UR * WR) {
+    int32_t jr = wr;
+    for (; jr + (UR - 1) * WR < nr; jr += UR * WR) {
       V v[UR];
 #pragma unroll
       for (int u = 0; u < UR; ++u)
-        v[u] = vload<true, T, VEC>(x + (j + u * WR) * sd + k0);
+        v[u] = vload<true, T, VEC>(base + int64_t(jr + u * WR) * sd);
 #pragma unroll
       for (int u = 0; u < UR; ++u)
 #pragma unroll
         for (int i = 0; i < VEC; ++i)
-          a[i].add(static_cast<O>(v[u].v[i]), j + u * WR);
+          la[i].add(static_cast<O>(v[u].v[i]), jr + u * WR);
     }
-    for (; j < j1; j += WR) {
-      const V v = vload<true, T, VEC>(x + j * sd + k0);
+    for (; jr < nr; jr += WR) {
+      const V v = vload<true, T, VEC>(base + int64_t(jr) * sd);
 #pragma unroll
       for (int i = 0; i < VEC; ++i)
-        a[i].add(static_cast<O>(v.v[i]), j);
+        la[i].add(static_cast<O>(v.v[i]), jr);
     }
   } else if (k0 < K) {
-    for (int64_t j = j0 + wr; j < j1; j += WR)
+    for (int32_t jr = wr; jr < nr; jr += WR)
       for (int i = 0; i < VEC; ++i)
         if (k0 + i < K)
-          a[i].add(static_cast<O>(x[j * sd + k0 + i]), j);
+          la[i].add(static_cast<O>(base[int64_t(jr) * sd + i]), jr);
   }
+  Acc a[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+    a[i] = ColLocal<Acc>::widen(la[i], j0);
   if constexpr (WR > 1) {
     // Wave rows of one column group merge in wave-row order.
 #pragma unroll
@@ -503,7 +551,8 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
   const bool drop_contig =
       p.drop.ndim == 0 || (p.drop.ndim == 1 && p.drop.strides[0] == 1);
   const bool col_layout = p.drop.ndim == 1 && p.keep.ndim == 1 &&
-                          p.keep.strides[0] == 1 && p.drop.strides[0] != 1;
+                          p.keep.strides[0] == 1 && p.drop.strides[0] != 1 &&
+                          p.D < (int64_t(1) << 31);
 
   if (FAST && drop_contig) {
     // Vector loads need every slice start and segment start VEC-aligned.
