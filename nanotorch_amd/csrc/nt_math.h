@@ -12,8 +12,8 @@ namespace nt {
 // device library's powf / pow (about 150 instructions per element, which
 // makes the pow kernels compute-bound).  Small integer and half-integer
 // exponents, |e| <= 4.5, take a short exact-operation path instead:
-//   e = n      : x^|n| by square-and-multiply (<= 3 roundings), 1/r if n < 0
-//   e = n + .5 : |x^n * sqrt(x)| (sqrt correctly rounded), 1/r if e < 0
+//   e = n      : x^|n| from x*x (<= 2 roundings), 1/r if n < 0
+//   e = n + .5 : |x^n * sqrt(x)| (fp32: hardware sqrt, 1 ulp), 1/r if e < 0
 // Both stay within 4 ulp of the correctly rounded power while every step is
 // a normal number.  Any other case -- a zero, subnormal, infinite or NaN
 // intermediate or result, which covers x = +-0, +-inf, NaN, x < 0 with a
@@ -41,24 +41,17 @@ inline PowPlan make_pow_plan(double e) {
   return p;
 }
 
-__device__ __forceinline__ float dev_sqrt(float a) { return sqrtf(a); }
+// Square root for the pow fast path.  fp32: the hardware v_sqrt_f32 (1 ulp,
+// one instruction; the correctly rounded sqrtf is a ~40-instruction
+// refinement, most of the fast path's cost).  Callers pass normal inputs only.
+// fp64: the correctly rounded sqrt.
+__device__ __forceinline__ float dev_sqrt(float a) {
+  return __builtin_amdgcn_sqrtf(a);
+}
 __device__ __forceinline__ double dev_sqrt(double a) { return sqrt(a); }
 __device__ __forceinline__ float dev_pow(float a, float e) { return powf(a, e); }
 __device__ __forceinline__ double dev_pow(double a, double e) {
   return pow(a, e);
-}
-
-template <class T> __device__ __forceinline__ T ipow_small(T x, int n) {
-  T r = T(1);
-  T b = x;
-  while (n > 0) {
-    if (n & 1)
-      r = r * b;
-    n >>= 1;
-    if (n)
-      b = b * b;
-  }
-  return r;
 }
 
 template <class T> __device__ __forceinline__ bool is_normal_num(T v) {
@@ -67,16 +60,31 @@ template <class T> __device__ __forceinline__ bool is_normal_num(T v) {
          a <= std::numeric_limits<T>::max();
 }
 
+// x^n for 0 <= n <= 4 with straight-line code (n is uniform across the
+// launch): x*x, (x*x)*x, (x*x)*(x*x) -- at most two roundings.
+template <class T> __device__ __forceinline__ T ipow4(T x, int n) {
+  const T x2 = x * x;
+  const T lo = n == 0 ? T(1) : x;
+  const T hi = n == 2 ? x2 : (n == 3 ? x2 * x : x2 * x2);
+  return n < 2 ? lo : hi;
+}
+
 template <class T>
 __device__ __forceinline__ T pow_planned(T x, T e, const PowPlan &p) {
+  if (p.mode == 1 && p.n == 0)
+    return T(1); // pow(x, +-0) = 1 for every x, NaN included
   if (p.mode != 0) {
-    if (p.n == 0 && p.mode == 1)
-      return T(1);
-    T r = ipow_small(x, p.n);
-    if (p.mode == 2)
-      r = std::fabs(r * dev_sqrt(x));
+    T r = ipow4(x, p.n);
+    if (p.mode == 2) // x must be normal for dev_sqrt (else r becomes NaN)
+      r = is_normal_num(x) ? std::fabs(r * dev_sqrt(x))
+                           : std::numeric_limits<T>::quiet_NaN();
     const T res = p.neg ? T(1) / r : r;
-    if (is_normal_num(x) && is_normal_num(r) && is_normal_num(res))
+    // A zero, subnormal, infinite or NaN intermediate or result (x = 0,
+    // inf, NaN, x < 0 under a square root, overflow, underflow) takes the
+    // library pow below.
+    // (Marked unlikely so that the library call's code is laid out after
+    // the kernel's hot path instead of between its unrolled elements.)
+    if (__builtin_expect(is_normal_num(r) && is_normal_num(res), 1))
       return res;
   }
   return dev_pow(x, e);
