@@ -245,6 +245,37 @@ int nt_reduce_bwd(int32_t op, const nt_view *g, double scale, const nt_view *idx
 int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
               int32_t accumulate);
 
+/* --------------------------------------------------------------- indexing */
+
+/* Replaces `gather_from_axes` (src/cpp/ops/copy_ops.cu:93-160, host only in
+ * the reference): out (any strides, x's dtype) = x indexed along the view
+ * axes fancy_dims_in_src[q] by the int64 arrays index_arrays[q], which all
+ * have one shape (the broadcast index shape, any strides).  Output axis i
+ * walks index axis out_axis_target[i] when out_axis_is_fancy[i], else view
+ * axis out_axis_target[i] -- the plan of the reference's _FancyAxes
+ * (src/nanotorch/core.py:667-774).  Indices must already be normalised to
+ * [0, axis length); one outside sets NT_ERR_INDEX and its element is not
+ * read.  Synchronizes the stream (to report that check). */
+int nt_gather_axes(const nt_view *x, const nt_view *out, int32_t nfancy,
+                   const int32_t *fancy_dims_in_src,
+                   const nt_view *index_arrays,
+                   const int32_t *out_axis_is_fancy,
+                   const int32_t *out_axis_target);
+
+/* Replaces `scatter_to_axes` (src/cpp/ops/copy_ops.cu:7-91): out indexed as
+ * in nt_gather_axes = src, src having the plan's output shape (any strides,
+ * stride 0 for broadcast values).  out is the indexed view itself (the
+ * reference passes the whole tensor, which is only right when no basic
+ * selector moved the view).  keep, when not NULL, is a bool array of the
+ * index shape: positions with keep = 0 are skipped, which the caller uses to
+ * keep only the last occurrence of a repeated index tuple (the reference's
+ * sequential last-write-wins).  Synchronizes the stream. */
+int nt_scatter_axes(const nt_view *src, const nt_view *out, int32_t nfancy,
+                    const int32_t *fancy_dims_in_src,
+                    const nt_view *index_arrays,
+                    const int32_t *out_axis_is_fancy,
+                    const int32_t *out_axis_target, const nt_view *keep);
+
 /* ------------------------------------------------------------- host utils */
 
 /* Replaces `manual_seed` / `uniform` (src/cpp/random.h:5-13,

@@ -79,6 +79,14 @@ _SIGNATURES = {
         [c_int32, _VP, c_double, _VP, _VP, POINTER(c_int64), c_int32, _VP, c_int32],
     ),
     "nt_matmul": (c_int, [_VP, _VP, _VP, c_int32]),
+    "nt_gather_axes": (
+        c_int,
+        [_VP, _VP, c_int32, POINTER(c_int32), _VP, POINTER(c_int32), POINTER(c_int32)],
+    ),
+    "nt_scatter_axes": (
+        c_int,
+        [_VP, _VP, c_int32, POINTER(c_int32), _VP, POINTER(c_int32), POINTER(c_int32), _VP],
+    ),
     "nt_manual_seed": (c_int, [c_uint64]),
     "nt_host_uniform": (c_int, [c_void_p, c_int32, c_int64, c_double, c_double]),
     "nt_event_create": (c_int, [POINTER(c_void_p)]),

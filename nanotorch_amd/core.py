@@ -16,6 +16,7 @@ from __future__ import annotations
 import math
 from typing import TYPE_CHECKING, Any, Sequence
 
+from . import _fancy
 from . import _kernels as K
 from ._data_type import (
     Dtype,
@@ -155,9 +156,11 @@ class Tensor:
             raise IndexError(f"Too many indices ({len(index)}) for {self.ndim}D array.")
         index = expand_ellipsis(index, self.shape)
         if not is_contiguous_view(index):
-            raise NotImplementedError(
-                "Advanced (sequence / mask) indexing is not supported by nanotorch_amd."
-            )
+            # sequence / Tensor / mask selectors: a gathered copy
+            # (reference: core.py:186-203)
+            shape, strides, offset, new_index = _fancy.newview_indexing(self, index)
+            view = Tensor._new_view(self._storage, shape, strides, offset)
+            return _fancy.gather(view, _fancy.compute_plan(shape, new_index))
         view = _basic_index_view(self, index)
         return Tensor._new_view(self._storage, view[0], view[1], view[2])
 
@@ -169,25 +172,32 @@ class Tensor:
         if len([x for x in index if x is not None]) > self.ndim:
             raise IndexError(f"Too many indices ({len(index)}) for {self.ndim}D array.")
         index = expand_ellipsis(index, self.shape)
-        if not is_contiguous_view(index):
-            raise NotImplementedError(
-                "Advanced (sequence / mask) indexing is not supported by nanotorch_amd."
-            )
-        shape, strides, offset = _basic_index_view(self, index)
+        fancy = not is_contiguous_view(index)
+        if fancy:
+            shape, strides, offset, new_index = _fancy.newview_indexing(self, index)
+        else:
+            shape, strides, offset = _basic_index_view(self, index)
         if not isinstance(value, Tensor):
             value = Tensor(value, dtype=self.dtype, device=self.device)
         elif value.dtype != self.dtype:
             value = value.to(self.dtype)
         if value.device != self.device:
             value = value.to(self.device)
+        target = Tensor._new_view(self._storage, shape, strides, offset)
+        plan = _fancy.compute_plan(shape, new_index) if fancy else None
         try:
-            value = value.expand(*shape)
+            value = value.expand(*(plan.new_shape if fancy else shape))
         except ValueError as e:
             raise IndexError(str(e)) from e
         if value._storage is self._storage:  # aliasing guard
             value = value._to_contiguous(force=True)
-        target = Tensor._new_view(self._storage, shape, strides, offset)
-        K.copy_view(value, target)
+        if fancy:
+            # scattered into the indexed view itself (the reference hands the
+            # whole tensor to scatter_to_axes, core.py:246-253, which is only
+            # right when no basic selector moved the view)
+            _fancy.scatter(value, target, plan)
+        else:
+            K.copy_view(value, target)
         self._storage.bump_version()
 
     # -- properties --------------------------------------------------------------

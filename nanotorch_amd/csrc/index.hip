@@ -1,0 +1,330 @@
+// Advanced (sequence / mask) indexing: gather from and scatter to a view
+// along "fancy" axes selected by int64 index arrays.
+//
+// The plan (which axes are fancy, the output shape and where each output
+// axis comes from) is the reference's _FancyAxes (src/nanotorch/core.py:667-
+// 774), computed by the Python layer, which also normalises negative
+// indices, checks bounds and turns boolean masks into index lists (those
+// steps raise IndexError / RuntimeError exactly where the reference does).
+// The reference runs both loops on the host only (src/cpp/ops/copy_ops.cu:
+// 7-160, `_require_cpu`); here one work-item moves one element:
+//
+//   gather : out[o] = x[src(o)],  o over the contiguous output
+//   scatter: out[dst(s)] = src[s], s over the (broadcast) source
+//
+// With all index arrays broadcast to one index shape, output axis i either
+// walks index axis out_axis_target[i] (fancy) or view axis out_axis_target[i]
+// (basic); view axis d takes idx_p[flat index coordinate] when it is the
+// p-th fancy axis.  A scatter whose index tuples repeat writes each target
+// once, from the last occurrence in row-major order (the reference's
+// sequential "last write wins"): the host marks, per index position,
+// whether it is the last occurrence of its tuple (`keep`).
+#include "ew_engine.h"
+
+extern "C" int nt_fill(void *data, int32_t dtype, int64_t n, double value);
+extern "C" const char *nt_last_error(void);
+
+namespace nt {
+
+constexpr int IDX_MAX_FANCY = NT_MAX_DIMS;
+
+struct IndexPlan {
+  int out_ndim;    // dims of the iteration space (gather: out, scatter: src)
+  int view_ndim;   // dims of the indexed view
+  int ind_ndim;    // dims of the broadcast index shape
+  int nfancy;
+  int64_t shape[NT_MAX_DIMS];      // iteration-space shape
+  FastDivU32 fd[NT_MAX_DIMS];      // its divisors (32-bit indexing)
+  int is_fancy[NT_MAX_DIMS];       // per iteration axis
+  int target[NT_MAX_DIMS];         // index axis (fancy) or view axis (basic)
+  int fancy_slot[NT_MAX_DIMS];     // per view axis: p, or -1 for basic
+  int64_t view_shape[NT_MAX_DIMS];
+  int64_t view_strides[NT_MAX_DIMS];
+  int64_t view_offset;
+  int64_t iter_strides[NT_MAX_DIMS]; // the other operand's strides over the
+  int64_t iter_offset;               // iteration space (out: contiguous)
+  int64_t ind_strides[IDX_MAX_FANCY][NT_MAX_DIMS]; // per index array
+  const int64_t *ind[IDX_MAX_FANCY];
+  const uint8_t *keep; // scatter: last-occurrence mask, contiguous over the
+  int64_t keep_strides[NT_MAX_DIMS]; // index shape (may be null)
+};
+
+// Offsets of iteration element `it` in the indexed view and in the other
+// operand; false when a scatter skips it (an earlier repeat of a tuple) or
+// an index lies outside its axis (then *err is set; the host checks every
+// index before the call, this keeps a bad C-ABI call from touching memory
+// outside the view).
+template <bool IDX32>
+__device__ __forceinline__ bool index_offsets(const IndexPlan &p, int64_t it,
+                                              int64_t &view_off,
+                                              int64_t &iter_off, int *err) {
+  int64_t loc_ind[NT_MAX_DIMS];
+  int64_t loc_basic[NT_MAX_DIMS];
+  int64_t io = p.iter_offset;
+  if constexpr (IDX32) {
+    uint32_t rem = uint32_t(it);
+    for (int d = p.out_ndim - 1; d >= 0; --d) {
+      const uint32_t q = p.fd[d].div(rem);
+      const int64_t c = int64_t(rem - q * uint32_t(p.shape[d]));
+      rem = q;
+      io += c * p.iter_strides[d];
+      if (p.is_fancy[d])
+        loc_ind[p.target[d]] = c;
+      else
+        loc_basic[p.target[d]] = c;
+    }
+  } else {
+    int64_t rem = it;
+    for (int d = p.out_ndim - 1; d >= 0; --d) {
+      const int64_t q = rem / p.shape[d];
+      const int64_t c = rem - q * p.shape[d];
+      rem = q;
+      io += c * p.iter_strides[d];
+      if (p.is_fancy[d])
+        loc_ind[p.target[d]] = c;
+      else
+        loc_basic[p.target[d]] = c;
+    }
+  }
+  if (p.keep) {
+    int64_t ko = 0;
+    for (int d = 0; d < p.ind_ndim; ++d)
+      ko += loc_ind[d] * p.keep_strides[d];
+    if (!p.keep[ko])
+      return false;
+  }
+  int64_t vo = p.view_offset;
+  for (int d = 0; d < p.view_ndim; ++d) {
+    const int slot = p.fancy_slot[d];
+    int64_t c;
+    if (slot < 0) {
+      c = loc_basic[d];
+    } else {
+      int64_t fo = 0;
+      for (int e = 0; e < p.ind_ndim; ++e)
+        fo += loc_ind[e] * p.ind_strides[slot][e];
+      c = p.ind[slot][fo];
+      if (c < 0 || c >= p.view_shape[d]) {
+        atomicOr(err, 1);
+        iter_off = io;
+        return false;
+      }
+    }
+    vo += c * p.view_strides[d];
+  }
+  view_off = vo;
+  iter_off = io;
+  return true;
+}
+
+template <class T, bool IDX32>
+__global__ __launch_bounds__(256) void gather_kernel(const T *__restrict__ x,
+                                                     T *__restrict__ out,
+                                                     IndexPlan p, int64_t n,
+                                                     int *err) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t it = int64_t(blockIdx.x) * 256 + threadIdx.x; it < n;
+       it += stride) {
+    int64_t vo = 0, io = 0;
+    const bool ok = index_offsets<IDX32>(p, it, vo, io, err);
+    out[io] = ok ? x[vo] : T(0);
+  }
+}
+
+template <class T, bool IDX32>
+__global__ __launch_bounds__(256) void scatter_kernel(const T *__restrict__ src,
+                                                      T *__restrict__ out,
+                                                      IndexPlan p, int64_t n,
+                                                      int *err) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t it = int64_t(blockIdx.x) * 256 + threadIdx.x; it < n;
+       it += stride) {
+    int64_t vo = 0, io = 0;
+    if (index_offsets<IDX32>(p, it, vo, io, err))
+      out[vo] = src[io];
+  }
+}
+
+namespace {
+
+// Validates the plan's arrays and fills everything but the iteration
+// operand.  `iter` is the iteration space (gather: out, scatter: src).
+IndexPlan make_index_plan(const nt_view *view, const nt_view *iter,
+                          int32_t nfancy, const int32_t *fancy_dims,
+                          const nt_view *index_arrays,
+                          const int32_t *out_axis_is_fancy,
+                          const int32_t *out_axis_target,
+                          const nt_view *keep) {
+  IndexPlan p{};
+  if (nfancy < 1 || nfancy > IDX_MAX_FANCY)
+    fail(NT_ERR_RUNTIME, "indexing: bad number of index arrays");
+  p.out_ndim = iter->ndim;
+  p.view_ndim = view->ndim;
+  p.nfancy = nfancy;
+  p.ind_ndim = index_arrays[0].ndim;
+  for (int d = 0; d < NT_MAX_DIMS; ++d)
+    p.fancy_slot[d] = -1;
+  for (int q = 0; q < nfancy; ++q) {
+    const nt_view &iv = index_arrays[q];
+    check_view(&iv, "indexing");
+    if (iv.dtype != NT_INT64)
+      fail(NT_ERR_RUNTIME, "indexing: index arrays must be int64");
+    if (iv.ndim != p.ind_ndim)
+      fail(NT_ERR_RUNTIME, "indexing: index arrays of different ranks");
+    for (int d = 0; d < p.ind_ndim; ++d) {
+      if (iv.shape[d] != index_arrays[0].shape[d])
+        fail(NT_ERR_RUNTIME, "indexing: index arrays of different shapes");
+      p.ind_strides[q][d] = iv.strides[d];
+    }
+    p.ind[q] = typed_ptr<const int64_t>(&iv);
+    const int d = fancy_dims[q];
+    if (d < 0 || d >= view->ndim || p.fancy_slot[d] != -1)
+      fail(NT_ERR_RUNTIME, "indexing: bad fancy axis");
+    p.fancy_slot[d] = q;
+  }
+  for (int i = 0; i < iter->ndim; ++i) {
+    p.shape[i] = iter->shape[i];
+    p.is_fancy[i] = out_axis_is_fancy[i] ? 1 : 0;
+    p.target[i] = out_axis_target[i];
+    const int lim = p.is_fancy[i] ? p.ind_ndim : view->ndim;
+    if (p.target[i] < 0 || p.target[i] >= lim)
+      fail(NT_ERR_RUNTIME, "indexing: bad axis plan");
+    const int64_t ext = p.is_fancy[i] ? index_arrays[0].shape[p.target[i]]
+                                      : view->shape[p.target[i]];
+    if (ext != p.shape[i])
+      fail(NT_ERR_RUNTIME, "indexing: shape does not match the axis plan");
+    p.iter_strides[i] = iter->strides[i];
+  }
+  // every basic view axis and every index axis is walked by exactly one
+  // iteration axis (otherwise a coordinate would be left undefined)
+  int basic_seen[NT_MAX_DIMS] = {}, ind_seen[NT_MAX_DIMS] = {};
+  for (int i = 0; i < iter->ndim; ++i) {
+    if (p.is_fancy[i])
+      ++ind_seen[p.target[i]];
+    else if (p.fancy_slot[p.target[i]] >= 0)
+      fail(NT_ERR_RUNTIME, "indexing: a basic axis of the plan is fancy");
+    else
+      ++basic_seen[p.target[i]];
+  }
+  for (int d = 0; d < view->ndim; ++d)
+    if (p.fancy_slot[d] < 0 && basic_seen[d] != 1)
+      fail(NT_ERR_RUNTIME, "indexing: axis plan does not cover the view");
+  for (int d = 0; d < p.ind_ndim; ++d)
+    if (ind_seen[d] != 1)
+      fail(NT_ERR_RUNTIME, "indexing: axis plan does not cover the indices");
+  p.iter_offset = iter->offset;
+  for (int d = 0; d < view->ndim; ++d) {
+    p.view_shape[d] = view->shape[d];
+    p.view_strides[d] = view->strides[d];
+  }
+  p.view_offset = view->offset;
+  p.keep = nullptr;
+  if (keep) {
+    check_view(keep, "indexing");
+    if (keep->dtype != NT_BOOL || keep->ndim != p.ind_ndim)
+      fail(NT_ERR_RUNTIME, "indexing: bad keep mask");
+    for (int d = 0; d < p.ind_ndim; ++d) {
+      if (keep->shape[d] != index_arrays[0].shape[d])
+        fail(NT_ERR_RUNTIME, "indexing: bad keep mask");
+      p.keep_strides[d] = keep->strides[d];
+    }
+    p.keep = reinterpret_cast<const uint8_t *>(
+        static_cast<const char *>(keep->data) + keep->offset);
+  }
+  return p;
+}
+
+template <bool SCATTER>
+void run_index(const nt_view *data, const nt_view *iter, const IndexPlan &base) {
+  const int64_t n = numel(iter);
+  if (n == 0)
+    return;
+  IndexPlan p = base;
+  const bool idx32 = n < (int64_t(1) << 32);
+  if (idx32)
+    for (int d = 0; d < p.out_ndim; ++d)
+      p.fd[d] = FastDivU32(uint32_t(p.shape[d]));
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256,
+                                           int64_t(device_cu_count()) * 16);
+  hipStream_t st = stream();
+  int *err = static_cast<int *>(device_alloc(sizeof(int)));
+  const int frc = nt_fill(err, NT_INT32, 1, 0.0);
+  if (frc != NT_OK) {
+    device_free(err);
+    fail(frc, nt_last_error());
+  }
+  dispatch_all(data->dtype, [&]<class T>() {
+    // raw storage pointers: the plan carries both offsets
+    T *dptr = static_cast<T *>(const_cast<void *>(data->data));
+    T *iptr = static_cast<T *>(const_cast<void *>(iter->data));
+    if constexpr (SCATTER) {
+      if (idx32)
+        scatter_kernel<T, true><<<dim3(unsigned(blocks)), 256, 0, st>>>(
+            iptr, dptr, p, n, err);
+      else
+        scatter_kernel<T, false><<<dim3(unsigned(blocks)), 256, 0, st>>>(
+            iptr, dptr, p, n, err);
+    } else {
+      if (idx32)
+        gather_kernel<T, true><<<dim3(unsigned(blocks)), 256, 0, st>>>(
+            dptr, iptr, p, n, err);
+      else
+        gather_kernel<T, false><<<dim3(unsigned(blocks)), 256, 0, st>>>(
+            dptr, iptr, p, n, err);
+    }
+  });
+  const hipError_t le = hipGetLastError();
+  int herr = 0;
+  const hipError_t ce =
+      le == hipSuccess
+          ? hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, st)
+          : le;
+  const hipError_t se = ce == hipSuccess ? hipStreamSynchronize(st) : ce;
+  device_free(err);
+  NT_HIP_CHECK(se);
+  if (herr)
+    fail(NT_ERR_INDEX, "index out of range for its axis");
+}
+
+} // namespace
+} // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_gather_axes(const nt_view *x, const nt_view *out, int32_t nfancy,
+                   const int32_t *fancy_dims_in_src,
+                   const nt_view *index_arrays,
+                   const int32_t *out_axis_is_fancy,
+                   const int32_t *out_axis_target) {
+  return guard([&] {
+    check_view(x, "gather_from_axes");
+    check_view(out, "gather_from_axes");
+    if (x->dtype != out->dtype)
+      fail(NT_ERR_RUNTIME, "gather_from_axes: dtype mismatch");
+    const IndexPlan p =
+        make_index_plan(x, out, nfancy, fancy_dims_in_src, index_arrays,
+                        out_axis_is_fancy, out_axis_target, nullptr);
+    run_index<false>(x, out, p);
+  });
+}
+
+int nt_scatter_axes(const nt_view *src, const nt_view *out, int32_t nfancy,
+                    const int32_t *fancy_dims_in_src,
+                    const nt_view *index_arrays,
+                    const int32_t *out_axis_is_fancy,
+                    const int32_t *out_axis_target, const nt_view *keep) {
+  return guard([&] {
+    check_view(src, "scatter_to_axes");
+    check_view(out, "scatter_to_axes");
+    if (src->dtype != out->dtype)
+      fail(NT_ERR_RUNTIME, "scatter_to_axes: dtype mismatch");
+    const IndexPlan p =
+        make_index_plan(out, src, nfancy, fancy_dims_in_src, index_arrays,
+                        out_axis_is_fancy, out_axis_target, keep);
+    run_index<true>(out, src, p);
+  });
+}
+
+} // extern "C"

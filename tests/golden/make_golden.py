@@ -165,6 +165,85 @@ def autograd_tables():
     ]
 
 
+def indexing_tables():
+    """Advanced indexing known answers, tests/test_ops/test_tensor_core.py.
+    Selectors are encoded as {"list": v} (a Python sequence), {"tensor": v}
+    (nt.tensor(v)), {"int": n}, {"slice": [start, stop, step]}, {"ellipsis": 1}
+    or {"none": 1}; "x" is nt.tensor(x) unless "arange" gives
+    nt.arange(n).reshape(shape)."""
+    M = [[1, 2, 3, 4], [5, 6, 7, 8], [9, 10, 11, 12]]
+    M3 = [[[1, 2], [3, 4]], [[5, 6], [7, 8]], [[9, 10], [11, 12]]]
+    L = lambda v: {"list": v}  # noqa: E731
+    T = lambda v: {"tensor": v}  # noqa: E731
+    S = lambda a=None, b=None, c=None: {"slice": [a, b, c]}  # noqa: E731
+    R12 = [[1, 2, 3, 4], [5, 6, 7, 8], [9, 10, 11, 12]][1:]
+    get = [
+        (":400-402", M, [L([1, 2])], R12),
+        (":405-407", M, [T([1, 2])], R12),
+        (":410-412", M, [L([False, True, True])], R12),
+        (":415-417", M, [T([False, True, True])], R12),
+        (":426-428", M, [L([-2, -1])], R12),
+        (":431-433", M, [T([-2, -1])], R12),
+        (":436-438", M, [S(), L([1, 2])], [[2, 3], [6, 7], [10, 11]]),
+        (":441-443", M, [S(), T([1, 2])], [[2, 3], [6, 7], [10, 11]]),
+        (":458-460", M, [L([1, 2, 1]), L([1, 1, 0])], [6, 10, 5]),
+        (":463-465", M, [T([1, 2, 1]), T([1, 1, 0])], [6, 10, 5]),
+        (":474-476", M, [L([1, 2, 1]), L([1])], [6, 10, 6]),
+        (":479-481", M, [L([1]), L([1, 2, 1])], [6, 7, 6]),
+        (":484-489", M, [L([[0, 1], [1, 2]])],
+         [[[1, 2, 3, 4], [5, 6, 7, 8]], [[5, 6, 7, 8], [9, 10, 11, 12]]]),
+        (":492-497", M, [T([[0, 1], [1, 2]])],
+         [[[1, 2, 3, 4], [5, 6, 7, 8]], [[5, 6, 7, 8], [9, 10, 11, 12]]]),
+        (":500-502", M3, [L([1, 1]), S(), L([1, 0])], [[6, 8], [5, 7]]),
+        (":505-507", M3, [T([1, 1]), S(), T([1, 0])], [[6, 8], [5, 7]]),
+    ]
+    out = []
+    for src, x, idx, exp in get:
+        out.append({"src": "tests/test_ops/test_tensor_core.py" + src, "kind": "get",
+                    "x": x, "index": idx, "expected": exp})
+    out.append({"src": "tests/test_ops/test_tensor_core.py:446-449", "kind": "get",
+                "x": M, "index": [L([])], "expected": [], "shape": [0, 4]})
+    for src, idx, err in [(":420-423", [L([False, True])], "IndexError"),
+                          (":468-471", [L([1, 2, 1]), L([1, 1, 0, 1])], "RuntimeError")]:
+        out.append({"src": "tests/test_ops/test_tensor_core.py" + src, "kind": "get",
+                    "x": M, "index": idx, "error": err})
+    for idx in ([L([1, 4]), {"int": 2}, L([2, 3])], [L([1, -5])]):  # :509-514
+        out.append({"src": "tests/test_ops/test_tensor_core.py:510-515", "kind": "get",
+                    "arange": 60, "shape": [4, 3, 5], "index": idx, "error": "IndexError"})
+    sets = [
+        (":655-658", 6, [6], [L([True, False, False, True, False, True])], 12,
+         [12, 1, 2, 12, 4, 12]),
+        (":667-670", 6, [6], [L([1, 3, 5])], 12, [0, 12, 2, 12, 4, 12]),
+        (":673-676", 6, [6], [T([1, 3, 5])], 12, [0, 12, 2, 12, 4, 12]),
+        (":679-682", 6, [6], [L([1, 3, -1])], 12, [0, 12, 2, 12, 4, 12]),
+        (":685-688", 6, [6], [L([0, 0, 0])], [12, 13, 14], [14, 1, 2, 3, 4, 5]),
+        (":798-801", 12, [4, 3], [L([True, False, False, True])], 12,
+         [[12, 12, 12], [3, 4, 5], [6, 7, 8], [12, 12, 12]]),
+        (":810-813", 12, [4, 3], [L([0, 3])], 12,
+         [[12, 12, 12], [3, 4, 5], [6, 7, 8], [12, 12, 12]]),
+        (":816-819", 12, [4, 3], [L([0, -1])], 12,
+         [[12, 12, 12], [3, 4, 5], [6, 7, 8], [12, 12, 12]]),
+        (":828-831", 12, [3, 4], [S(), L([1, 2])], [[10, 20], [30, 40], [50, 60]],
+         [[0, 10, 20, 3], [4, 30, 40, 7], [8, 50, 60, 11]]),
+        (":834-837", 12, [3, 4], [L([[0, 1], [1, 2]])], 33,
+         [[33, 33, 33, 33], [33, 33, 33, 33], [33, 33, 33, 33]]),
+        (":840-843", 12, [3, 4], [L([0, 1]), L([1, 2])], 33,
+         [[0, 33, 2, 3], [4, 5, 33, 7], [8, 9, 10, 11]]),
+    ]
+    for src, n, shape, idx, val, exp in sets:
+        out.append({"src": "tests/test_ops/test_tensor_core.py" + src, "kind": "set",
+                    "arange": n, "shape": shape, "index": idx, "value": val,
+                    "expected": exp})
+    for src, n, shape, idx in [(":661-664", 6, [6], [L([True, False, False, True, False])]),
+                               (":691-694", 6, [6], [L([1, 3, 5, 12])]),
+                               (":804-807", 12, [4, 3], [L([True, False, False])]),
+                               (":822-825", 12, [4, 3], [L([0, 4])])]:
+        out.append({"src": "tests/test_ops/test_tensor_core.py" + src, "kind": "set",
+                    "arange": n, "shape": shape, "index": idx, "value": 12,
+                    "error": "IndexError"})
+    return out
+
+
 def main() -> None:
     mm, a23 = matmul_tables()
     data = {
@@ -174,6 +253,7 @@ def main() -> None:
         "matmul_a23": a23,
         "reduction": reduction_tables(),
         "autograd": autograd_tables(),
+        "indexing": indexing_tables(),
         "rng": {"src": "tests/test_factories.py:239-242", "seed": 42,
                 "first": 0.7551555037498474,
                 "second_msvc": 0.6390313506126404,
