@@ -142,18 +142,16 @@ __device__ __forceinline__ float frag(const float *lds, int mn, int k) {
     return lds[mn * MM_KPAD + k];
 }
 
-template <int LA, int LB>
-__global__ __launch_bounds__(MM_THREADS, 2) void mm_f32_mfma_kernel(MMArgs g) {
-  __shared__ __align__(16) float lds[2][2][MM_REGION]; // [stage][A/B]
-  const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int h = lane >> 5, li = lane & 31;
+// Workgroup -> (batch, tile) with an XCD-contiguous numbering, then groups
+// of 8 tile-rows walked column by column; A, B, C advanced to the batch.
+struct TileCoord {
+  int64_t m0, n0;
+  const float *A, *B;
+  float *C;
+};
 
-  // ---- tile coordinates: XCD-contiguous numbering, then groups of 8
-  // tile-rows walked column by column.
-  const int64_t ntiles = g.tiles_m * g.tiles_n;
-  const int64_t per_batch = ntiles;
+__device__ __forceinline__ TileCoord mm_tile_coord(const MMArgs &g) {
+  const int64_t per_batch = g.tiles_m * g.tiles_n;
   int64_t bid = blockIdx.x;
   const int64_t nblk = gridDim.x;
   if (nblk % 8 == 0)
@@ -166,25 +164,60 @@ __global__ __launch_bounds__(MM_THREADS, 2) void mm_f32_mfma_kernel(MMArgs g) {
   const int64_t gsize = (g.tiles_m - first_m) < GROUP ? (g.tiles_m - first_m)
                                                        : GROUP;
   const int64_t in_group = tile - group * GROUP * g.tiles_n;
-  const int64_t tm = first_m + in_group % gsize;
-  const int64_t tn = in_group / gsize;
-  const int64_t m0 = tm * MM_BM, n0 = tn * MM_BN;
-
-  // ---- batch offsets
-  const float *A = g.A;
-  const float *B = g.B;
-  float *C = g.C;
-  {
-    int64_t rem = batch;
-    for (int d = g.nb - 1; d >= 0; --d) {
-      const int64_t q = rem / g.bshape[d];
-      const int64_t c = rem - q * g.bshape[d];
-      rem = q;
-      A += c * g.bsA[d];
-      B += c * g.bsB[d];
-      C += c * g.bsC[d];
-    }
+  TileCoord tc;
+  tc.m0 = (first_m + in_group % gsize) * MM_BM;
+  tc.n0 = (in_group / gsize) * MM_BN;
+  tc.A = g.A;
+  tc.B = g.B;
+  tc.C = g.C;
+  int64_t rem = batch;
+  for (int d = g.nb - 1; d >= 0; --d) {
+    const int64_t q = rem / g.bshape[d];
+    const int64_t c = rem - q * g.bshape[d];
+    rem = q;
+    tc.A += c * g.bsA[d];
+    tc.B += c * g.bsB[d];
+    tc.C += c * g.bsC[d];
   }
+  return tc;
+}
+
+// Lane holds column li of each 32x32 block, rows 8*(r/4) + 4*h + (r%4).
+__device__ __forceinline__ void mm_epilogue(const MMArgs &g, const TileCoord &tc,
+                                            const floatx16 (&acc)[2][2], int wm,
+                                            int wn, int h, int li) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = tc.n0 + wn * 64 + j * 32 + li;
+      if (col >= g.N)
+        continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row =
+            tc.m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        if (row < g.M) {
+          float *dst = tc.C + row * g.sCm + col * g.sCn;
+          const float v = acc[i][j][r];
+          *dst = g.accumulate ? (*dst + v) : v;
+        }
+      }
+    }
+}
+
+template <int LA, int LB>
+__global__ __launch_bounds__(MM_THREADS, 2) void mm_f32_mfma_kernel(MMArgs g) {
+  __shared__ __align__(16) float lds[2][2][MM_REGION]; // [stage][A/B]
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int h = lane >> 5, li = lane & 31;
+
+  const TileCoord tc = mm_tile_coord(g);
+  const int64_t m0 = tc.m0, n0 = tc.n0;
+  const float *A = tc.A;
+  const float *B = tc.B;
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -236,26 +269,158 @@ __global__ __launch_bounds__(MM_THREADS, 2) void mm_f32_mfma_kernel(MMArgs g) {
     __syncthreads();
   }
 
-  // ---- epilogue: lane holds column li of each 32x32 block, rows
-  // 8*(r/4) + 4*h + (r%4).
+  mm_epilogue(g, tc, acc, wm, wn, h, li);
+}
+
+// ------------------------------------------ direct-to-LDS staging (gfx950)
+
+// gfx950 can move 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane L of a wave lands at LDS base + 16 L, with
+// the base wave-uniform.  The kernel below stages both operands that way --
+// no VGPR round trip, no LDS store instructions -- when both are in a vector
+// layout and K is a multiple of the 32-deep k-tile.  Each wave instruction
+// fills 1 KB of a stage:
+//   layout K : the stage is [128 mn][32 k] without padding; 16-byte chunk c
+//              of row r sits at chunk c ^ (r % 8), so the fragment reads
+//              (8 lanes, 8 rows, one chunk each) hit all 32 banks.  One
+//              instruction covers 8 rows.
+//   layout MN: the stage is [32 k][128 mn]; one instruction covers 2 k rows.
+// Rows (columns) past M (N) re-read the last valid one: their results are
+// never stored.
+constexpr int DL_STAGE = 128 * 32; // floats per operand stage
+
+template <int LAY> struct DirectTile {
+  const float *src[4]; // this work-item's source for instruction j, k-tile 0
+  int64_t kstep;       // elements between two k-tiles
+  __device__ __forceinline__ void init(const float *p, int64_t mn0, int64_t MN,
+                                       int64_t s_mn, int64_t s_k, int wave,
+                                       int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (LAY == LAY_K) {
+        const int r = (wave * 4 + j) * 8 + lane / 8;
+        const int c = (lane % 8) ^ ((lane / 8) & 7);
+        const int64_t row = mn0 + r < MN ? mn0 + r : MN - 1;
+        src[j] = p + row * s_mn + 4 * c;
+      } else {
+        const int kr = (wave * 4 + j) * 2 + lane / 32;
+        const int64_t mn = mn0 + 4 * (lane % 32) <= MN - 4
+                               ? mn0 + 4 * (lane % 32)
+                               : MN - 4;
+        src[j] = p + kr * s_k + mn;
+      }
+    }
+    kstep = LAY == LAY_K ? 32 : 32 * s_k;
+  }
+  __device__ __forceinline__ void issue(float *stage, int64_t kt,
+                                        int wave) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)(src[j] + kt * kstep),
+          (__attribute__((address_space(3))) void *)(stage +
+                                                     (wave * 4 + j) * 256),
+          16, 0, 0);
+  }
+};
+
+// f[i][kk] = element (mn + 32 i, h * 16 + kk) of a direct-loaded stage.
+template <int LAY>
+__device__ __forceinline__ void dl_frags(const float *stage, int mn, int li,
+                                         int h, float (&f)[2][16]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = mn + 32 * i + li;
+    if constexpr (LAY == LAY_K) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int pc = (4 * h + q) ^ (li & 7);
+        const float4 w =
+            *reinterpret_cast<const float4 *>(stage + row * 32 + pc * 4);
+        f[i][4 * q + 0] = w.x;
+        f[i][4 * q + 1] = w.y;
+        f[i][4 * q + 2] = w.z;
+        f[i][4 * q + 3] = w.w;
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk)
+        f[i][kk] = stage[(h * 16 + kk) * 128 + row];
+    }
+  }
+}
+
+template <int LA, int LB>
+__device__ __forceinline__ void dl_compute(const float *sa, const float *sb,
+                                           int wm, int wn, int li, int h,
+                                           floatx16 (&acc)[2][2]) {
+  float fa[2][16], fb[2][16];
+  dl_frags<LA>(sa, wm * 64, li, h, fa);
+  dl_frags<LB>(sb, wn * 64, li, h, fb);
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][kk], fb[j][kk],
+                                                         acc[i][j], 0, 0, 0);
+}
+
+__device__ __forceinline__ void dl_wait_and_sync() {
+  // the stage's direct loads have landed in LDS, then every wave sees them
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+// Same tiling and MFMA schedule as mm_f32_mfma_kernel, operands staged by
+// direct loads into two named stage pairs (the k loop is unrolled by two so
+// that every LDS access names its stage at compile time).
+template <int LA, int LB>
+__global__ __launch_bounds__(MM_THREADS, 2) void mm_f32_mfma_dl_kernel(
+    MMArgs g) {
+  __shared__ __align__(16) float sA0[DL_STAGE], sB0[DL_STAGE];
+  __shared__ __align__(16) float sA1[DL_STAGE], sB1[DL_STAGE];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int h = lane >> 5, li = lane & 31;
+  const TileCoord tc = mm_tile_coord(g);
+
+  floatx16 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn * 64 + j * 32 + li;
-      if (col >= g.N)
-        continue;
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row =
-            m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-        if (row < g.M) {
-          float *dst = C + row * g.sCm + col * g.sCn;
-          const float v = acc[i][j][r];
-          *dst = g.accumulate ? (*dst + v) : v;
-        }
-      }
+      for (int r = 0; r < 16; ++r)
+        acc[i][j][r] = 0.f;
+
+  DirectTile<LA> ta;
+  DirectTile<LB> tb;
+  ta.init(tc.A, tc.m0, g.M, g.sAm, g.sAk, wave, lane);
+  tb.init(tc.B, tc.n0, g.N, g.sBn, g.sBk, wave, lane);
+  const int64_t ktiles = g.K / 32;
+  ta.issue(sA0, 0, wave);
+  tb.issue(sB0, 0, wave);
+  dl_wait_and_sync();
+  for (int64_t kt = 0; kt < ktiles; kt += 2) {
+    if (kt + 1 < ktiles) {
+      ta.issue(sA1, kt + 1, wave);
+      tb.issue(sB1, kt + 1, wave);
     }
+    dl_compute<LA, LB>(sA0, sB0, wm, wn, li, h, acc);
+    dl_wait_and_sync();
+    if (kt + 1 >= ktiles)
+      break;
+    if (kt + 2 < ktiles) {
+      ta.issue(sA0, kt + 2, wave);
+      tb.issue(sB0, kt + 2, wave);
+    }
+    dl_compute<LA, LB>(sA1, sB1, wm, wn, li, h, acc);
+    dl_wait_and_sync();
+  }
+  mm_epilogue(g, tc, acc, wm, wn, h, li);
 }
 
 // ------------------------------------------------ SIMT (non-fp32) kernel
@@ -312,6 +477,13 @@ __global__ __launch_bounds__(256) void mm_simt_kernel(MMArgsT<T> g) {
 namespace {
 
 template <int LA, int LB> void launch_mfma(const MMArgs &a, int64_t blocks) {
+  if constexpr (LA != LAY_GEN && LB != LAY_GEN) {
+    if (a.K % 32 == 0) {
+      mm_f32_mfma_dl_kernel<LA, LB>
+          <<<dim3(unsigned(blocks)), MM_THREADS, 0, stream()>>>(a);
+      return;
+    }
+  }
   mm_f32_mfma_kernel<LA, LB>
       <<<dim3(unsigned(blocks)), MM_THREADS, 0, stream()>>>(a);
 }
