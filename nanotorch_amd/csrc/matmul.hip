@@ -30,6 +30,10 @@
 // bound).  Accumulate mode adds C_old after the full dot product: one
 // rounding, like the reference's `x._grad += grad`.
 //
+// When both operands are in a vector layout and K is a multiple of 32, the
+// operands skip the register round trip: mm_f32_mfma_dl_kernel stages them
+// with gfx950's direct global-to-LDS loads (same tiles, same MFMA schedule).
+//
 // Other dtypes (fp64, int32, int64) use a tiled SIMT kernel that accumulates
 // in k order exactly like the reference's CPU loop (matmul.cu:33-45).
 #include <algorithm>
