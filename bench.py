@@ -383,6 +383,51 @@ def cpu_baseline(rows: int = 1024) -> dict:
             "host_cpu": cpu, "host_nproc": os.cpu_count()}
 
 
+def cpu_parts() -> dict:
+    """The oracle (the reference's CPU kernels restated) on bounded samples
+    of configs 1, 3 and 4, on this host's cores: single-threaded like the
+    reference, plus the bit-identical OpenMP matmul on all cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    r = np.random.default_rng(9)
+    out: dict = {"cores_available": os.cpu_count(), "threads_omp": O.threads()}
+    # config 3 sample: [1024, 8192] (1/8 of the rows)
+    x = r.standard_normal((1024, 8192)).astype(np.float32)
+    red = {}
+    for name, op, dt in (("sum", O.R_SUM, np.float32), ("max", O.R_MAX, None)):
+        for label, axes in (("axis0", (0,)), ("axis1", (1,)), ("full", (0, 1))):
+            t0 = time.perf_counter()
+            O.reduce(op, x, axes, dt)
+            dt_s = time.perf_counter() - t0
+            red[f"{name}|{label}|fwd"] = round(x.nbytes / dt_s / 1e9, 3)
+    out["reductions_GB/s_1thread"] = red
+    out["reductions_sample"] = "[1024, 8192] fp32 (1/8 of config 3)"
+    # config 4 sample: 512^3 single thread, 1024^3 on all cores
+    mm = {}
+    for n, par in ((512, False), (1024, True)):
+        a = r.standard_normal((n, n)).astype(np.float32)
+        b = (r.standard_normal((n, n)) / np.sqrt(n)).astype(np.float32)
+        t0 = time.perf_counter()
+        O.matmul(a, b, parallel=par)
+        dt_s = time.perf_counter() - t0
+        mm[f"{n}^3|{'omp' if par else '1thread'}"] = round(2 * n**3 / dt_s / 1e9, 3)
+    out["matmul_GFLOP/s"] = mm
+    # config 1: the 2-layer MLP step, single thread
+    X = r.standard_normal((64, 784)).astype(np.float32)
+    T = np.eye(10, dtype=np.float32)[r.integers(0, 10, 64)]
+    params = [((r.standard_normal((784, 256)) * np.sqrt(2 / 784)).astype(np.float32),
+               np.zeros(256, np.float32)),
+              ((r.standard_normal((256, 10)) * np.sqrt(2 / 256)).astype(np.float32),
+               np.zeros(10, np.float32))]
+    t0 = time.perf_counter()
+    steps = 5
+    for _ in range(steps):
+        O.mlp_step(params, X, T, ["relu"], 0.01, parallel=False)
+    out["mlp_config1_step/s_1thread"] = round(steps / (time.perf_counter() - t0), 2)
+    return out
+
+
 # ---------------------------------------------------------------- profiles
 
 _PROF = "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/{d} -o run -- python -u bench.py {a}"
@@ -392,6 +437,10 @@ PROFILE_CMDS = {
     "red": _PROF.format(d="prof_red", a="--parts red"),
     "mm": _PROF.format(d="prof_mm", a="--parts mm"),
     "mlp": _PROF.format(d="prof_mlp", a="--parts mlp --mlp-steps 5"),
+    "mm_pmc": _PMC.format(
+        c="SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_WAVE_CYCLES "
+          "SQ_WAIT_INST_LDS SQ_LDS_BANK_CONFLICT",
+        d="prof_mm_pmc", a="--parts mm"),
     "fetch": _PMC.format(c="FETCH_SIZE", d="prof_fetch", a="--steps 1 --warmup 0 --parts ew --calib"),
     "write": _PMC.format(c="WRITE_SIZE", d="prof_write", a="--steps 1 --warmup 0 --parts ew --calib"),
 }
@@ -424,6 +473,47 @@ def _sweep_key(name: str):
     return f"{opn}|{layout}|{'fwd' if kind.endswith('Fwd') else 'bwd'}"
 
 
+def _summarize_mm_pmc(path: str, out_md: str) -> None:
+    """MFMA-pipe utilisation per matmul kernel and grid: busy cycles of the
+    matrix pipe summed over the 1024 SIMDs, over SIMDs x duration x clock."""
+    import csv
+    simds, clock_ghz = 256 * 4, 2.4
+    per: dict[tuple, dict] = {}
+    for r in csv.DictReader(open(os.path.join(path, "run_counter_collection.csv"))):
+        if "mfma" not in r["Kernel_Name"]:
+            continue
+        key = (_short(r["Kernel_Name"]), int(r["Grid_Size"]))
+        d = per.setdefault(key, {"dispatch": {}})
+        disp = d["dispatch"].setdefault(r["Dispatch_Id"], {
+            "dur_ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+        disp[r["Counter_Name"]] = float(r["Counter_Value"])
+    rows = []
+    for (name, grid), d in sorted(per.items()):
+        ds = list(d["dispatch"].values())
+        avg = lambda k: sum(x.get(k, 0.0) for x in ds) / len(ds)  # noqa: E731
+        dur = avg("dur_ns")
+        busy = avg("SQ_VALU_MFMA_BUSY_CYCLES")
+        util = busy / (simds * dur * clock_ghz) if dur else 0.0
+        rows.append((name, grid, len(ds), dur / 1e3, avg("SQ_INSTS_MFMA"), busy, util,
+                     avg("SQ_WAIT_INST_LDS") / max(avg("SQ_WAVE_CYCLES"), 1.0),
+                     avg("SQ_LDS_BANK_CONFLICT")))
+    with open(out_md, "w") as o:
+        o.write("# MFMA-pipe utilisation: config-4 matmul kernels\n\n")
+        o.write(f"Command (repo root on the GPU box):\n\n```\n{PROFILE_CMDS['mm_pmc']}\n```\n\n")
+        o.write("Summarised with `python bench.py --summarize mm_pmc gpurun_out/prof_mm_pmc`. "
+                "Utilisation = SQ_VALU_MFMA_BUSY_CYCLES (summed over the 1024 SIMDs) / "
+                "(1024 x kernel duration x 2.4 GHz); each v_mfma_f32_32x32x2_f32 keeps the "
+                "pipe busy 64 cycles, so this equals achieved / peak FLOP rate at 2.4 GHz. "
+                "Grid 262144 work-items = 4096x4096 outputs, 524288 = 8192x4096. "
+                "Durations are from this (counter-collecting) run.\n\n")
+        o.write("| kernel | grid | dispatches | avg us | MFMA instr | MFMA busy cycles | "
+                "MFMA util | LDS-wait / wave cycles | LDS bank conflicts |\n"
+                "|---|---|---|---|---|---|---|---|---|\n")
+        for name, grid, n, us, inst, busy, util, lw, bc in rows:
+            o.write(f"| `{name}` | {grid} | {n} | {us:.1f} | {inst:.0f} | {busy:.3g} | "
+                    f"{util:.3f} | {lw:.3f} | {bc:.0f} |\n")
+
+
 def summarize(kind: str, dirs: list[str]) -> None:
     import csv
     prof = os.path.join(ROOT, "profiles")
@@ -443,6 +533,9 @@ def summarize(kind: str, dirs: list[str]) -> None:
                      f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
         with open(os.path.join(prof, fname), "w") as f:
             f.write("\n".join(o) + "\n")
+        return
+    if kind == "mm_pmc":
+        _summarize_mm_pmc(dirs[0], os.path.join(prof, "matmul_config4_mfma_utilisation.md"))
         return
     if kind != "traffic":
         raise SystemExit(f"unknown profile kind {kind}")
@@ -502,7 +595,7 @@ def main() -> int:
                          "written each): the reference dispatch for HBM byte counters")
     ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
                     help="write a profiles/ summary from rocprofv3 csv output: "
-                         "sweep|red|mm|mlp DIR, or traffic FETCH_DIR WRITE_DIR")
+                         "sweep|red|mm|mlp|mm_pmc DIR, or traffic FETCH_DIR WRITE_DIR")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize[0], args.summarize[1:])
@@ -579,6 +672,7 @@ def main() -> int:
         line["parts"]["mlp"] = bench_mlp(args.mlp_steps)
     if "cpu" in parts:
         line["cpu_baseline"] = cpu_baseline()
+        line["parts"]["cpu_reference"] = cpu_parts()
     else:
         line["cpu_baseline"] = None
     line["host"] = platform.node()

@@ -284,14 +284,21 @@ __global__ __launch_bounds__(MM_THREADS, 2) void mm_f32_mfma_kernel(MMArgs g) {
 // no VGPR round trip, no LDS store instructions -- when both are in a vector
 // layout and K is a multiple of the 32-deep k-tile.  Each wave instruction
 // fills 1 KB of a stage:
-//   layout K : the stage is [128 mn][32 k] without padding; 16-byte chunk c
-//              of row r sits at chunk c ^ (r % 8), so the fragment reads
-//              (8 lanes, 8 rows, one chunk each) hit all 32 banks.  One
-//              instruction covers 8 rows.
+//   layout K : the stage is [128 mn][32 k] without padding, 16-byte chunks
+//              swizzled within a row (dl_swz) so that fragment reads are
+//              bank-conflict free.  One instruction covers 8 rows.
 //   layout MN: the stage is [32 k][128 mn]; one instruction covers 2 k rows.
 // Rows (columns) past M (N) re-read the last valid one: their results are
 // never stored.
 constexpr int DL_STAGE = 128 * 32; // floats per operand stage
+
+// Chunk swizzle of a [mn][k] stage row.  A fragment read is a 16-byte read
+// per lane of one chunk from 16 consecutive rows (lanes li of a half-wave);
+// gfx950's LDS serves 16 lanes x 16 bytes over its 64 banks at once, so the
+// 16 (row parity, chunk) pairs must differ: chunk c of row r is stored at
+// c ^ (r % 8) ^ ((r / 8) % 2).  (With c ^ (r % 8) alone, rows r and r + 8
+// collide: rocprof counted one LDS bank conflict per read.)
+__device__ __forceinline__ int dl_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 template <int LAY> struct DirectTile {
   const float *src[4]; // this work-item's source for instruction j, k-tile 0
@@ -303,7 +310,7 @@ template <int LAY> struct DirectTile {
     for (int j = 0; j < 4; ++j) {
       if constexpr (LAY == LAY_K) {
         const int r = (wave * 4 + j) * 8 + lane / 8;
-        const int c = (lane % 8) ^ ((lane / 8) & 7);
+        const int c = (lane % 8) ^ dl_swz(r);
         const int64_t row = mn0 + r < MN ? mn0 + r : MN - 1;
         src[j] = p + row * s_mn + 4 * c;
       } else {
@@ -338,7 +345,7 @@ __device__ __forceinline__ void dl_frags(const float *stage, int mn, int li,
     if constexpr (LAY == LAY_K) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int pc = (4 * h + q) ^ (li & 7);
+        const int pc = (4 * h + q) ^ dl_swz(row);
         const float4 w =
             *reinterpret_cast<const float4 *>(stage + row * 32 + pc * 4);
         f[i][4 * q + 0] = w.x;
