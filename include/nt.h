@@ -287,7 +287,8 @@ int nt_host_uniform(void *host_out, int32_t dtype, int64_t n, double low,
                     double high);
 
 /* Timing events on the library stream (no reference counterpart; used by the
- * benchmark to time kernels on the stream they run on). */
+ * benchmark to time kernels on the stream they run on).  Timing-only events:
+ * recording one orders nothing for the host or other devices. */
 int nt_event_create(void **ev);
 int nt_event_record(void *ev);
 int nt_event_elapsed_ms(void *start, void *end, float *ms);

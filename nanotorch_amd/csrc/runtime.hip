@@ -394,7 +394,9 @@ int nt_host_uniform(void *host_out, int32_t dtype, int64_t n, double low,
 int nt_event_create(void **ev) {
   return guard([&] {
     hipEvent_t e;
-    NT_HIP_CHECK(hipEventCreate(&e));
+    // Timing only: no system-scope release at record time, so a bracket
+    // around one launch does not add an L2 write-back to what it measures.
+    NT_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
     *ev = reinterpret_cast<void *>(e);
   });
 }

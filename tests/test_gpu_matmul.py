@@ -35,7 +35,10 @@ def _check(got, a, b, what):
 
 
 SHAPES = [(1, 1, 1), (2, 3, 4), (5, 7, 3), (32, 32, 32), (128, 128, 128), (129, 33, 130),
-          (257, 100, 63), (64, 1000, 96), (300, 257, 511), (1024, 512, 768)]
+          (257, 100, 63), (64, 1000, 96), (300, 257, 511), (1024, 512, 768),
+          # K % 32 == 0 with ragged M / N (multiples of 4): the direct-to-LDS
+          # kernel's clamped edge tiles, every layout pair
+          (132, 96, 260), (36, 64, 100), (1000, 256, 1004), (4, 32, 4)]
 
 
 @pytest.mark.parametrize("layout", ["NN", "TN", "NT", "TT"])
@@ -61,6 +64,10 @@ def test_matmul_generic_strides_and_batch(gpu):
     xb = dev(b).expand(4, 3, 19, 23)
     got = _mm(dev(a), xb)
     _check(got, a, np.broadcast_to(b, (4, 3, 19, 23)), "batched+bcast")
+    # batched, vector layouts, K % 32 == 0 (direct-to-LDS kernel)
+    a = r.standard_normal((2, 3, 68, 64)).astype(np.float32)
+    b = r.standard_normal((2, 3, 64, 132)).astype(np.float32)
+    _check(_mm(dev(a), dev(b)), a, b, "batched direct")
     del b
 
 
