@@ -39,6 +39,22 @@ namespace nt {
 constexpr int RED_THREADS = 256;
 constexpr int RED_WAVES = RED_THREADS / 64;
 
+// Column-walk shape (reduce_col_kernel): rows in flight per work-item, wave
+// columns per workgroup on wide tensors, workgroups per CU for sums and for
+// max/min.
+#ifndef NT_COL_UR
+#define NT_COL_UR 8
+#endif
+#ifndef NT_COL_WC
+#define NT_COL_WC 4
+#endif
+#ifndef NT_COL_WG_SUM
+#define NT_COL_WG_SUM 1
+#endif
+#ifndef NT_COL_WG_SEL
+#define NT_COL_WG_SEL 2
+#endif
+
 // ------------------------------------------------------------ accumulators
 
 template <class O> struct SumAcc {
@@ -56,8 +72,8 @@ template <class O> struct SumAcc {
 
 template <class O, bool IS_MAX> struct SelAcc {
   O v;
+  int32_t c; // before j: a float accumulator packs into 16 bytes
   int64_t j;
-  int32_t c;
   __device__ __forceinline__ void init() {
     v = IS_MAX ? std::numeric_limits<O>::lowest()
                : std::numeric_limits<O>::max();
@@ -597,16 +613,18 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
         reinterpret_cast<uintptr_t>(xp) % (sizeof(T) * VEC) == 0 &&
         sd % VEC == 0;
     const int vec = aligned ? VEC : 1;
-    // Wide tensors: 4 waves side by side (64 * vec * 4 columns per
+    // Wide tensors: WC waves side by side (64 * vec * WC columns per
     // workgroup); narrow ones: 1 column group, 4 wave rows.
-    constexpr int UR = 8;
-    const int wc = K >= 4 * 64 * vec ? 4 : 1;
+    constexpr int UR = NT_COL_UR;
+    constexpr int WC = NT_COL_WC;
+    const int wc = K >= WC * 64 * vec ? WC : 1;
     const int64_t bx = ceil_div(K, int64_t(64) * vec * wc);
     // About one (sum) or two (max/min, larger partials) workgroups per CU:
     // fewer, longer row walks with UR loads in flight measured faster than
     // many short ones, and keep the partials small.
     const int64_t col_target =
-        int64_t(device_cu_count()) * (sizeof(Acc) <= 8 ? 1 : 2);
+        int64_t(device_cu_count()) *
+        (sizeof(Acc) <= 8 ? NT_COL_WG_SUM : NT_COL_WG_SEL);
     int64_t S = std::max<int64_t>(1, ceil_div(col_target, bx));
     S = std::min<int64_t>(S, std::max<int64_t>(1, D / (UR * (RED_WAVES / wc))));
     S = std::min<int64_t>(S, 65535);
@@ -618,14 +636,14 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
     if (bx >= (int64_t(1) << 31))
       fail(NT_ERR_RUNTIME, "reduction too large");
     const dim3 grid{unsigned(bx), unsigned(S), 1u};
-    if (aligned && wc == 4)
-      reduce_col_kernel<T, O, Acc, VEC, 4, UR, MODE>
+    if (aligned && wc == WC)
+      reduce_col_kernel<T, O, Acc, VEC, WC, UR, MODE>
           <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
     else if (aligned)
       reduce_col_kernel<T, O, Acc, VEC, 1, UR, MODE>
           <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
-    else if (wc == 4)
-      reduce_col_kernel<T, O, Acc, 1, 4, UR, MODE>
+    else if (wc == WC)
+      reduce_col_kernel<T, O, Acc, 1, WC, UR, MODE>
           <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
     else
       reduce_col_kernel<T, O, Acc, 1, 1, UR, MODE>
