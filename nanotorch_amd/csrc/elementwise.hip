@@ -307,7 +307,8 @@ int nt_equals(const nt_view *a, const nt_view *b, int32_t *result) {
       const nt_view *outs[1] = {&mv};
       launch_elementwise<T, bool, 2, 1>(ins, outs, NotEqualFlag<T>{});
     });
-    NT_HIP_CHECK(hipMemsetAsync(flag, 0, sizeof(int), stream()));
+    if (nt_fill(flag, NT_INT32, 1, 0.0) != NT_OK)
+      fail(NT_ERR_RUNTIME, nt_last_error());
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
     any_true_kernel<<<dim3(unsigned(blocks)), 256, 0, stream()>>>(
         static_cast<const bool *>(mask), n, static_cast<int *>(flag));

@@ -555,7 +555,8 @@ int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
         dispatch_arith(c->dtype, [&]<class T>() {
           // C = 0 through the copy kernel from a broadcast zero.
           T *zero = static_cast<T *>(device_alloc(sizeof(T)));
-          NT_HIP_CHECK(hipMemsetAsync(zero, 0, sizeof(T), stream()));
+          if (nt_fill(zero, c->dtype, 1, 0.0) != NT_OK)
+            fail(NT_ERR_RUNTIME, nt_last_error());
           nt_view zv = *c;
           zv.data = zero;
           zv.offset = 0;
