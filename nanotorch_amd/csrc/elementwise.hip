@@ -290,8 +290,9 @@ int nt_equals(const nt_view *a, const nt_view *b, int32_t *result) {
       return;
     }
     // Materialise a != b as a bool mask, then OR-reduce it into a flag.
-    void *mask = device_alloc(size_t(n));
-    void *flag = device_alloc(sizeof(int));
+    DeviceScratch mask_buf{size_t(n)}, flag_buf{sizeof(int)};
+    void *mask = mask_buf.get();
+    void *flag = flag_buf.get();
     nt_view mv{};
     mv.data = mask;
     mv.dtype = NT_BOOL;
@@ -317,8 +318,6 @@ int nt_equals(const nt_view *a, const nt_view *b, int32_t *result) {
     NT_HIP_CHECK(hipMemcpyAsync(&host_flag, flag, sizeof(int),
                                 hipMemcpyDeviceToHost, stream()));
     NT_HIP_CHECK(hipStreamSynchronize(stream()));
-    device_free(mask);
-    device_free(flag);
     *result = host_flag ? 0 : 1;
   });
 }

@@ -247,12 +247,11 @@ void run_index(const nt_view *data, const nt_view *iter, const IndexPlan &base) 
   const int64_t blocks = std::min<int64_t>((n + 255) / 256,
                                            int64_t(device_cu_count()) * 16);
   hipStream_t st = stream();
-  int *err = static_cast<int *>(device_alloc(sizeof(int)));
+  DeviceScratch err_buf(sizeof(int));
+  int *err = err_buf.get<int>();
   const int frc = nt_fill(err, NT_INT32, 1, 0.0);
-  if (frc != NT_OK) {
-    device_free(err);
+  if (frc != NT_OK)
     fail(frc, nt_last_error());
-  }
   dispatch_all(data->dtype, [&]<class T>() {
     // raw storage pointers: the plan carries both offsets
     T *dptr = static_cast<T *>(const_cast<void *>(data->data));
@@ -280,7 +279,6 @@ void run_index(const nt_view *data, const nt_view *iter, const IndexPlan &base) 
           ? hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, st)
           : le;
   const hipError_t se = ce == hipSuccess ? hipStreamSynchronize(st) : ce;
-  device_free(err);
   NT_HIP_CHECK(se);
   if (herr)
     fail(NT_ERR_INDEX, "index out of range for its axis");

@@ -554,7 +554,8 @@ int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
       if (!accumulate) {
         dispatch_arith(c->dtype, [&]<class T>() {
           // C = 0 through the copy kernel from a broadcast zero.
-          T *zero = static_cast<T *>(device_alloc(sizeof(T)));
+          DeviceScratch zero_buf(sizeof(T));
+          T *zero = zero_buf.get<T>();
           if (nt_fill(zero, c->dtype, 1, 0.0) != NT_OK)
             fail(NT_ERR_RUNTIME, nt_last_error());
           nt_view zv = *c;
@@ -563,7 +564,6 @@ int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
           for (int d = 0; d < zv.ndim; ++d)
             zv.strides[d] = 0;
           const int rc = nt_copy(&zv, c);
-          device_free(zero);
           if (rc != NT_OK)
             fail(rc, nt_last_error());
         });

@@ -36,6 +36,26 @@ int device_cu_count();
 void *device_alloc(size_t nbytes);
 void device_free(void *p);
 
+// Scoped scratch buffer, returned to the caching allocator when the scope
+// ends -- also when a check throws.  All work runs on the library stream and
+// the allocator hands a freed block only to later work on that stream, so
+// freeing while a queued kernel still uses the buffer is safe.
+class DeviceScratch {
+public:
+  explicit DeviceScratch(size_t nbytes)
+      : p_(nbytes ? device_alloc(nbytes) : nullptr) {}
+  ~DeviceScratch() {
+    if (p_)
+      device_free(p_);
+  }
+  DeviceScratch(const DeviceScratch &) = delete;
+  DeviceScratch &operator=(const DeviceScratch &) = delete;
+  template <class T = void> T *get() const { return static_cast<T *>(p_); }
+
+private:
+  void *p_;
+};
+
 #define NT_HIP_CHECK(expr)                                                     \
   do {                                                                         \
     hipError_t e_ = (expr);                                                    \

@@ -560,8 +560,6 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
             <<<dim3(unsigned(p.K)), RED_THREADS, 0, st>>>(partial, S, out);
       NT_LAUNCH_CHECK();
     }
-    if (partial)
-      device_free(partial);
   };
 
   const bool drop_contig =
@@ -586,9 +584,8 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
     int64_t seg = ceil_div(p.D, S);
     seg = ceil_div(seg, VEC) * VEC;
     S = ceil_div(p.D, seg);
-    Acc *partial =
-        S > 1 ? static_cast<Acc *>(device_alloc(sizeof(Acc) * p.K * S))
-              : nullptr;
+    DeviceScratch partial_buf(S > 1 ? sizeof(Acc) * p.K * S : 0);
+    Acc *partial = partial_buf.get<Acc>();
     const KeepDesc kd = to_keep_desc(p.keep);
     const int64_t blocks = p.K * S;
     if (blocks >= (int64_t(1) << 31))
@@ -630,9 +627,8 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
     S = std::min<int64_t>(S, 65535);
     const int64_t seg = ceil_div(D, S);
     S = ceil_div(D, seg);
-    Acc *partial =
-        S > 1 ? static_cast<Acc *>(device_alloc(sizeof(Acc) * K * S))
-              : nullptr;
+    DeviceScratch partial_buf(S > 1 ? sizeof(Acc) * K * S : 0);
+    Acc *partial = partial_buf.get<Acc>();
     if (bx >= (int64_t(1) << 31))
       fail(NT_ERR_RUNTIME, "reduction too large");
     const dim3 grid{unsigned(bx), unsigned(S), 1u};
@@ -655,8 +651,6 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
               partial, K, int(S), out);
       NT_LAUNCH_CHECK();
     }
-    if (partial)
-      device_free(partial);
     return;
   }
 
@@ -677,9 +671,8 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
   S = std::max<int64_t>(1, std::min<int64_t>(S, 1 << 16));
   const int64_t seg = ceil_div(p.D, S);
   S = ceil_div(p.D, seg);
-  Acc *partial = S > 1
-                     ? static_cast<Acc *>(device_alloc(sizeof(Acc) * p.K * S))
-                     : nullptr;
+  DeviceScratch partial_buf(S > 1 ? sizeof(Acc) * p.K * S : 0);
+  Acc *partial = partial_buf.get<Acc>();
   const int64_t blocks = p.K * S;
   if (blocks >= (int64_t(1) << 31))
     fail(NT_ERR_RUNTIME, "reduction too large");
