@@ -53,11 +53,13 @@ class SumOp(Function):
         new_shape = _out_shape(x, self._axis, keepdim)
         self._x_dtype = x.dtype
         self._dtype = dtype
+        # set before the empty case too (the reference sets it after, so its
+        # backward through an empty sum fails, ops_reduction.py:60-64)
+        self._orig_shape = x.shape
         if x.is_empty:
             return Tensor._new_contiguous(
                 K.fill(math.prod(new_shape), 0, dtype, x.device), new_shape
             )
-        self._orig_shape = x.shape
         st = K.reduce(_lib.R_SUM, x, self._axis, dtype)
         return Tensor._new_contiguous(st, new_shape)
 
@@ -156,6 +158,7 @@ class _SelectOp(Function):
     """Shared max/min: forward keeps (value, first index, tie count)."""
 
     _op: int
+    _empty_shape = None  # input shape when the input was empty
 
     def forward(self, x: Tensor, axis=None, keepdim: bool = False) -> Tensor:
         self._axis = broadcast_axis(axis, x)
@@ -166,6 +169,9 @@ class _SelectOp(Function):
                 raise IndexError(
                     "argmin() expects reduction dim to be specified for numel=0."
                 )
+            # backward returns an empty gradient (the reference's would read
+            # the input shape it never recorded)
+            self._empty_shape = x.shape
             return Tensor._new_contiguous(
                 K.fill(math.prod(new_shape), 0, x.dtype, x.device), new_shape
             )
@@ -182,7 +188,12 @@ class _SelectOp(Function):
             self._op, g, 1.0, self._idx, self._cnt, self._axis, self._orig_shape, target
         )
 
+    def _empty_grad(self, g: Tensor) -> Tensor:
+        return Tensor._new_contiguous(K.fill(0, 0, g.dtype, g.device), self._empty_shape)
+
     def backward(self, grad_out: Tensor) -> tuple[Tensor, ...]:
+        if self._empty_shape is not None:
+            return (self._empty_grad(grad_out),)
         if not self._orig_shape:
             return (grad_out,)
         return (Tensor._new_contiguous(self._grad(grad_out, None), self._orig_shape),)
@@ -193,6 +204,8 @@ class _SelectOp(Function):
     def _backward_into(self, g: Tensor, needs, targets):
         if not needs[0]:
             return [None]
+        if self._empty_shape is not None:
+            return [targets[0] if targets[0] is not None else self._empty_grad(g)]
         if not self._orig_shape:
             if targets[0] is None:
                 return [g]

@@ -17,10 +17,26 @@ from .function import Function
 from .ops_utils import unbroadcast
 
 
+def _empty_passthrough(op: Function, x: Tensor) -> Tensor:
+    """Forward of an empty input: the input itself, as the reference returns
+    it.  The op saves nothing, so its backward passes the (empty) gradient
+    through (the reference's backward would read saved tensors that were
+    never saved)."""
+    op._empty = True
+    return x
+
+
+def _empty_backward_into(g: Tensor, needs, targets) -> list:
+    if not needs[0]:
+        return [None] * len(needs)
+    return [targets[0] if targets[0] is not None else g] + [None] * (len(needs) - 1)
+
+
 class _UnaryOp(Function):
     _op: int
     _promote = True  # float-only op: integer inputs become float32
     _in_dtype = None
+    _empty = False
 
     def _prepare(self, x: Tensor) -> Tensor:
         self._in_dtype = x.dtype
@@ -29,6 +45,8 @@ class _UnaryOp(Function):
         return x
 
     def fused_ok(self) -> bool:
+        if self._empty:
+            return True
         return is_float(self._in_dtype) and getattr(self, "_saved_ok", True)
 
     def _fused_saved(self):
@@ -38,6 +56,8 @@ class _UnaryOp(Function):
         return 0.0
 
     def _backward_into(self, g: Tensor, needs, targets):
+        if self._empty:
+            return _empty_backward_into(g, needs, targets)
         if not needs[0]:
             return [None]
         saved = self._fused_saved()
@@ -89,7 +109,7 @@ class ExpOp(_UnaryOp):
 
     def forward(self, x: Tensor) -> Tensor:
         if x.is_empty:
-            return x
+            return _empty_passthrough(self, x)
         x = self._prepare(x)
         y = Tensor._new_contiguous(K.unary(_lib.EXP, x), x.shape)
         self.save_for_backward(y)
@@ -106,7 +126,7 @@ class LogOp(_UnaryOp):
 
     def forward(self, x: Tensor) -> Tensor:
         if x.is_empty:
-            return x
+            return _empty_passthrough(self, x)
         x = self._prepare(x)
         self.save_for_backward(x)
         return Tensor._new_contiguous(K.unary(_lib.LOG, x), x.shape)
@@ -122,7 +142,7 @@ class SqrtOp(_UnaryOp):
 
     def forward(self, x: Tensor) -> Tensor:
         if x.is_empty:
-            return x
+            return _empty_passthrough(self, x)
         x = self._prepare(x)
         y = Tensor._new_contiguous(K.unary(_lib.SQRT, x), x.shape)
         self.save_for_backward(y)
@@ -140,7 +160,7 @@ class TanhOp(_UnaryOp):
 
     def forward(self, x: Tensor) -> Tensor:
         if x.is_empty:
-            return x
+            return _empty_passthrough(self, x)
         x = self._prepare(x)
         y = Tensor._new_contiguous(K.unary(_lib.TANH, x), x.shape)
         self.save_for_backward(y)
@@ -158,7 +178,7 @@ class SigmoidOp(_UnaryOp):
 
     def forward(self, x: Tensor) -> Tensor:
         if x.is_empty:
-            return x
+            return _empty_passthrough(self, x)
         x = self._prepare(x)
         y = Tensor._new_contiguous(K.unary(_lib.SIGMOID, x), x.shape)
         self.save_for_backward(y)
@@ -176,10 +196,11 @@ class PowOp(Function):
 
     _dtype = None
     _x_dtype = None
+    _empty = False
 
     def forward(self, x: Tensor, exponent) -> Tensor:
         if x.is_empty:
-            return x
+            return _empty_passthrough(self, x)
         if not isinstance(exponent, Tensor):
             exponent = Tensor(exponent)
         dtype = promote_dtypes(x.dtype, exponent.dtype)
@@ -197,9 +218,13 @@ class PowOp(Function):
         return (grad_out * exponent * x ** (exponent - 1),)
 
     def fused_ok(self) -> bool:
+        if self._empty:
+            return True
         return is_float(self._dtype) and self._x_dtype == self._dtype
 
     def _backward_into(self, g: Tensor, needs, targets):
+        if self._empty:
+            return _empty_backward_into(g, needs, targets)
         results = [None, None]
         if not needs[0]:
             return results
