@@ -327,6 +327,99 @@ def bench_mlp(steps: int = 20) -> dict:
             "loss_trace": [round(v, 7) for v in trace], "steps": steps}
 
 
+# --------------------------------------------- next rows beside the path
+
+
+def _index_args(fn: str, plan, first, second, keep_alive: list) -> list:
+    """ctypes arguments of nt_gather_axes / nt_scatter_axes for a fixed plan,
+    with the index arrays uploaded once (so the timed calls move no host
+    data)."""
+    import ctypes
+    nf = len(plan.fancy_dims_in_src)
+    idx = [nt.Tensor(a, dtype=nt.int64, device="cuda") for a in plan.index_arrays]
+    views = (_lib.NtView * nf)(*[K.view_of(t) for t in idx])
+    fd = (ctypes.c_int32 * nf)(*plan.fancy_dims_in_src)
+    nd = len(plan.new_shape)
+    isf = (ctypes.c_int32 * nd)(*[1 if b else 0 for b in plan.out_axis_is_fancy])
+    tgt = (ctypes.c_int32 * nd)(*plan.out_axis_target)
+    va, vb = K.view_of(first), K.view_of(second)
+    keep_alive += [idx, views, fd, isf, tgt, va, vb]
+    args = [ctypes.byref(va), ctypes.byref(vb), nf, fd, views, isf, tgt]
+    if fn == "nt_scatter_axes":
+        args.append(None)  # unique rows: no last-occurrence mask
+    return args
+
+
+def bench_next(iters: int = 10) -> dict:
+    """The rows next to the hot path, each timed per launch with HIP events
+    on the library stream: device casts and a comparison (no host round
+    trip), strided copy of a transposed view, a batched matmul on the MFMA
+    kernel, and advanced-index gather / scatter of rows.  Bytes are
+    algorithmic (every operand once); GB/s against the HBM peak, TFLOP/s
+    against the fp32 MFMA peak."""
+    from nanotorch_amd import _fancy
+    r = np.random.default_rng(6)
+    # [8192, 8192]: every case's operands exceed the 256 MB Infinity Cache,
+    # so back-to-back launches still stream from HBM
+    shape = (8192, 8192)
+    n = shape[0] * shape[1]
+    a = dev(r.standard_normal(shape).astype(np.float32))
+    b = dev(r.standard_normal(shape).astype(np.float32))
+    a64 = dev(r.standard_normal(shape))
+    lab = dev(r.integers(0, 1000, shape, dtype=np.int64))
+    o32, o64, ob = _fresh(shape), _fresh(shape, nt.float64), _fresh(shape, nt.bool_)
+    B, Mb = 16, 1024
+    xb = dev(r.standard_normal((B, Mb, Mb)).astype(np.float32))
+    yb = dev((r.standard_normal((B, Mb, Mb)) / np.sqrt(Mb)).astype(np.float32))
+    ob3 = _fresh((B, Mb, Mb))
+    rows, width = 50000, 1024
+    table = dev(r.standard_normal((rows, width)).astype(np.float32))
+    ids = r.permutation(rows)[:8192]
+    gplan = _fancy.compute_plan(table.shape, (ids.tolist(),))
+    gout = _fresh(gplan.new_shape)
+    keep: list = []
+    gargs = _index_args("nt_gather_axes", gplan, table, gout, keep)
+    sargs = _index_args("nt_scatter_axes", gplan, gout, table, keep)
+    import ctypes
+    vab, vbb, vob = view(a), view(b), view(ob)
+    cmp_args = (_lib.GT, ctypes.byref(vab), ctypes.byref(vbb), ctypes.byref(vob))
+    cases = {
+        # name: (launch, bytes or None, flop or None)
+        "cast|f32->f64": (lambda: K.copy_view(a, o64), 12 * n, None),
+        "cast|f64->f32": (lambda: K.copy_view(a64, o32), 12 * n, None),
+        "cast|i64->f32": (lambda: K.copy_view(lab, o32), 12 * n, None),
+        "compare|gt": (lambda: _lib.call("nt_binary", *cmp_args), 9 * n, None),
+        "copy|transposed": (lambda: K.copy_view(a.T, o32), 8 * n, None),
+        "matmul|batched 16x1024^3": (lambda: K.matmul_into(xb, yb, ob3, accumulate=False),
+                                     None, 2 * B * Mb**3),
+        "gather|8192 rows of [50000,1024]": (lambda: _lib.call("nt_gather_axes", *gargs),
+                                             2 * gout.numel * 4 + 8 * len(ids), None),
+        "scatter|8192 rows of [50000,1024]": (lambda: _lib.call("nt_scatter_axes", *sargs),
+                                              2 * gout.numel * 4 + 8 * len(ids), None),
+    }
+    out = {}
+    for name, (fn, nbytes, flop) in cases.items():
+        # back-to-back launches of one case between two events: the average
+        # launch, with the stream kept busy
+        fn()
+        e0, e1 = _lib.Event(), _lib.Event()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        nt.sync()
+        avg = e0.elapsed_ms(e1) / iters
+        if flop is not None:
+            tf = flop / (avg * 1e-3) / 1e12
+            out[name] = {"ms": round(avg, 5), "TFLOP/s": round(tf, 2),
+                         "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+        else:
+            gbs = nbytes / (avg * 1e-3) / 1e9
+            out[name] = {"ms": round(avg, 5), "GB/s": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline
 
 
@@ -437,6 +530,7 @@ PROFILE_CMDS = {
     "red": _PROF.format(d="prof_red", a="--parts red"),
     "mm": _PROF.format(d="prof_mm", a="--parts mm"),
     "mlp": _PROF.format(d="prof_mlp", a="--parts mlp --mlp-steps 5"),
+    "next": _PROF.format(d="prof_next", a="--parts next"),
     "mm_pmc": _PMC.format(
         c="SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_WAVE_CYCLES "
           "SQ_WAIT_INST_LDS SQ_LDS_BANK_CONFLICT",
@@ -449,6 +543,8 @@ PROFILE_FILES = {
     "red": ("reduce_config3_trace.md", "Kernel statistics: config-3 reductions [8192, 8192] fp32"),
     "mm": ("matmul_config4_trace.md", "Kernel statistics: config-4 MatMulOp forward + dA + dB"),
     "mlp": ("mlp_config5_trace.md", "Kernel statistics: config-5 4-layer MLP training steps"),
+    "next": ("next_rows_trace.md", "Kernel statistics: casts, comparison, strided copy, "
+                                   "batched matmul, gather / scatter (the rows beside the path)"),
 }
 _UN = {0: "exp", 1: "log", 2: "neg", 3: "relu", 4: "sqrt", 5: "tanh", 6: "sigmoid", 7: "pow"}
 _BI = {0: "add", 1: "sub", 2: "mul", 3: "truediv"}
@@ -588,14 +684,14 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--parts", default="all",
-                    help="all | none (the headline sweep only) | comma list of ew,red,mm,mlp,cpu")
+                    help="all | none (the headline sweep only) | comma list of ew,red,mm,mlp,next,cpu")
     ap.add_argument("--mlp-steps", type=int, default=20)
     ap.add_argument("--calib", action="store_true",
                     help="first run 3 plain copies of 2^24 fp32 (64 MiB read + 64 MiB "
                          "written each): the reference dispatch for HBM byte counters")
     ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
                     help="write a profiles/ summary from rocprofv3 csv output: "
-                         "sweep|red|mm|mlp|mm_pmc DIR, or traffic FETCH_DIR WRITE_DIR")
+                         "sweep|red|mm|mlp|next|mm_pmc DIR, or traffic FETCH_DIR WRITE_DIR")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize[0], args.summarize[1:])
@@ -608,7 +704,7 @@ def main() -> int:
     if not nt.is_available():
         print("no HIP device / libnt.so", file=sys.stderr)
         return 1
-    parts = {"ew", "red", "mm", "mlp", "cpu"} if args.parts == "all" else (
+    parts = {"ew", "red", "mm", "mlp", "next", "cpu"} if args.parts == "all" else (
         {"ew"} if args.parts == "none" else set(args.parts.split(",")))
 
     if args.calib:
@@ -627,6 +723,8 @@ def main() -> int:
             line["parts"]["matmul"] = bench_matmul()
         if "mlp" in parts:
             line["parts"]["mlp"] = bench_mlp(args.mlp_steps)
+        if "next" in parts:
+            line["parts"]["next_rows"] = bench_next()
         print(json.dumps(line), flush=True)
         return 0
 
@@ -670,6 +768,8 @@ def main() -> int:
         line["parts"]["matmul"] = bench_matmul()
     if "mlp" in parts:
         line["parts"]["mlp"] = bench_mlp(args.mlp_steps)
+    if "next" in parts:
+        line["parts"]["next_rows"] = bench_next()
     if "cpu" in parts:
         line["cpu_baseline"] = cpu_baseline()
         line["parts"]["cpu_reference"] = cpu_parts()

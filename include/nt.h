@@ -109,7 +109,9 @@ int nt_init(void);
  * Writes 1 if a HIP device can be used, else 0.  Never fails. */
 int nt_is_available(int *available);
 
-/* Replaces `cuda_sync()` (src/cpp/cuda.h:24-26, cuda.cpp:6). */
+/* Replaces `cuda_sync()` (src/cpp/cuda.h:24-26, cuda.cpp:6).  Also returns
+ * (once) NT_ERR_INDEX when an earlier gather/scatter met an out-of-range
+ * index; nt_memcpy_d2h does the same. */
 int nt_sync(void);
 
 /* Message of the last failing call on this thread ("" if none). */
@@ -254,8 +256,9 @@ int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
  * walks index axis out_axis_target[i] when out_axis_is_fancy[i], else view
  * axis out_axis_target[i] -- the plan of the reference's _FancyAxes
  * (src/nanotorch/core.py:667-774).  Indices must already be normalised to
- * [0, axis length); one outside sets NT_ERR_INDEX and its element is not
- * read.  Synchronizes the stream (to report that check). */
+ * [0, axis length).  The call only queues work.  An index outside its axis
+ * is caught on the device: its element is not read (out gets 0 there), and
+ * the next nt_sync() or nt_memcpy_d2h() returns NT_ERR_INDEX. */
 int nt_gather_axes(const nt_view *x, const nt_view *out, int32_t nfancy,
                    const int32_t *fancy_dims_in_src,
                    const nt_view *index_arrays,
@@ -269,7 +272,8 @@ int nt_gather_axes(const nt_view *x, const nt_view *out, int32_t nfancy,
  * selector moved the view).  keep, when not NULL, is a bool array of the
  * index shape: positions with keep = 0 are skipped, which the caller uses to
  * keep only the last occurrence of a repeated index tuple (the reference's
- * sequential last-write-wins).  Synchronizes the stream. */
+ * sequential last-write-wins).  An index outside its axis is skipped and
+ * reported as in nt_gather_axes. */
 int nt_scatter_axes(const nt_view *src, const nt_view *out, int32_t nfancy,
                     const int32_t *fancy_dims_in_src,
                     const nt_view *index_arrays,

@@ -7,7 +7,8 @@
 // indices, checks bounds and turns boolean masks into index lists (those
 // steps raise IndexError / RuntimeError exactly where the reference does).
 // The reference runs both loops on the host only (src/cpp/ops/copy_ops.cu:
-// 7-160, `_require_cpu`); here one work-item moves one element:
+// 7-160, `_require_cpu`); here one work-item moves one element, or one
+// 16-byte vector of the innermost axis when the layout allows:
 //
 //   gather : out[o] = x[src(o)],  o over the contiguous output
 //   scatter: out[dst(s)] = src[s], s over the (broadcast) source
@@ -21,8 +22,6 @@
 // whether it is the last occurrence of its tuple (`keep`).
 #include "ew_engine.h"
 
-extern "C" int nt_fill(void *data, int32_t dtype, int64_t n, double value);
-extern "C" const char *nt_last_error(void);
 
 namespace nt {
 
@@ -105,7 +104,7 @@ __device__ __forceinline__ bool index_offsets(const IndexPlan &p, int64_t it,
         fo += loc_ind[e] * p.ind_strides[slot][e];
       c = p.ind[slot][fo];
       if (c < 0 || c >= p.view_shape[d]) {
-        atomicOr(err, 1);
+        *err = NT_ERR_INDEX; // the deferred-error word (host memory)
         iter_off = io;
         return false;
       }
@@ -117,31 +116,45 @@ __device__ __forceinline__ bool index_offsets(const IndexPlan &p, int64_t it,
   return true;
 }
 
-template <class T, bool IDX32>
+// Work-item g moves VEC consecutive elements of the innermost iteration
+// axis (VEC > 1 only when that axis is basic, unit-stride in both operands
+// and a multiple of VEC long, and every vector is aligned: then the group's
+// offsets are those of its first element).
+template <class T, bool IDX32, int VEC>
 __global__ __launch_bounds__(256) void gather_kernel(const T *__restrict__ x,
                                                      T *__restrict__ out,
-                                                     IndexPlan p, int64_t n,
+                                                     IndexPlan p, int64_t ngroups,
                                                      int *err) {
+  using V = VecT<T, VEC>;
   const int64_t stride = int64_t(gridDim.x) * 256;
-  for (int64_t it = int64_t(blockIdx.x) * 256 + threadIdx.x; it < n;
-       it += stride) {
+  for (int64_t g = int64_t(blockIdx.x) * 256 + threadIdx.x; g < ngroups;
+       g += stride) {
     int64_t vo = 0, io = 0;
-    const bool ok = index_offsets<IDX32>(p, it, vo, io, err);
-    out[io] = ok ? x[vo] : T(0);
+    const bool ok = index_offsets<IDX32>(p, g * VEC, vo, io, err);
+    V v;
+    if (ok) {
+      v = *reinterpret_cast<const V *>(x + vo);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        v.v[j] = T(0);
+    }
+    *reinterpret_cast<V *>(out + io) = v;
   }
 }
 
-template <class T, bool IDX32>
+template <class T, bool IDX32, int VEC>
 __global__ __launch_bounds__(256) void scatter_kernel(const T *__restrict__ src,
                                                       T *__restrict__ out,
-                                                      IndexPlan p, int64_t n,
+                                                      IndexPlan p, int64_t ngroups,
                                                       int *err) {
+  using V = VecT<T, VEC>;
   const int64_t stride = int64_t(gridDim.x) * 256;
-  for (int64_t it = int64_t(blockIdx.x) * 256 + threadIdx.x; it < n;
-       it += stride) {
+  for (int64_t g = int64_t(blockIdx.x) * 256 + threadIdx.x; g < ngroups;
+       g += stride) {
     int64_t vo = 0, io = 0;
-    if (index_offsets<IDX32>(p, it, vo, io, err))
-      out[vo] = src[io];
+    if (index_offsets<IDX32>(p, g * VEC, vo, io, err))
+      *reinterpret_cast<V *>(out + vo) = *reinterpret_cast<const V *>(src + io);
   }
 }
 
@@ -234,6 +247,36 @@ IndexPlan make_index_plan(const nt_view *view, const nt_view *iter,
   return p;
 }
 
+// Vector width for the plan: VEC elements of the innermost iteration axis
+// per work-item when that axis is basic and unit-stride in both operands,
+// its length is a multiple of VEC, and every vector start is VEC-aligned
+// (every other stride a multiple of VEC, both bases aligned).
+template <class T>
+int index_vec(const nt_view *data, const nt_view *iter, const IndexPlan &p) {
+  constexpr int V = ew_vec<T>();
+  if (V == 1 || p.out_ndim == 0)
+    return 1;
+  const int last = p.out_ndim - 1;
+  if (p.is_fancy[last] || p.iter_strides[last] != 1 ||
+      p.view_strides[p.target[last]] != 1 || p.shape[last] % V != 0)
+    return 1;
+  for (int i = 0; i < last; ++i)
+    if (p.iter_strides[i] % V != 0)
+      return 1;
+  for (int d = 0; d < p.view_ndim; ++d)
+    if (p.view_strides[d] % V != 0 && d != p.target[last])
+      return 1;
+  const auto al = [&](const nt_view *v) {
+    return (reinterpret_cast<uintptr_t>(v->data) + uintptr_t(v->offset) * sizeof(T)) %
+               (V * sizeof(T)) == 0;
+  };
+  return al(data) && al(iter) ? V : 1;
+}
+
+// Queues the kernel and returns: an index outside its axis (possible only
+// for a caller that skipped the host-side checks) is skipped -- a gather
+// writes zeros there -- and stored in the deferred-error word, which the
+// next nt_sync / device-to-host copy raises as NT_ERR_INDEX.
 template <bool SCATTER>
 void run_index(const nt_view *data, const nt_view *iter, const IndexPlan &base) {
   const int64_t n = numel(iter);
@@ -244,44 +287,42 @@ void run_index(const nt_view *data, const nt_view *iter, const IndexPlan &base) 
   if (idx32)
     for (int d = 0; d < p.out_ndim; ++d)
       p.fd[d] = FastDivU32(uint32_t(p.shape[d]));
-  const int64_t blocks = std::min<int64_t>((n + 255) / 256,
-                                           int64_t(device_cu_count()) * 16);
   hipStream_t st = stream();
-  DeviceScratch err_buf(sizeof(int));
-  int *err = err_buf.get<int>();
-  const int frc = nt_fill(err, NT_INT32, 1, 0.0);
-  if (frc != NT_OK)
-    fail(frc, nt_last_error());
+  int *err = deferred_error_word();
   dispatch_all(data->dtype, [&]<class T>() {
     // raw storage pointers: the plan carries both offsets
     T *dptr = static_cast<T *>(const_cast<void *>(data->data));
     T *iptr = static_cast<T *>(const_cast<void *>(iter->data));
+    const int vec = index_vec<T>(data, iter, p);
+    const int64_t groups = n / vec;
+    const dim3 grid{unsigned(std::min<int64_t>((groups + 255) / 256,
+                                               int64_t(device_cu_count()) * 16)),
+                    1u, 1u};
+    constexpr int V = ew_vec<T>();
+#define NT_IDX_LAUNCH(K, A, B, I32, VV)                                        \
+  K<T, I32, VV><<<grid, 256, 0, st>>>(A, B, p, groups, err)
     if constexpr (SCATTER) {
-      if (idx32)
-        scatter_kernel<T, true><<<dim3(unsigned(blocks)), 256, 0, st>>>(
-            iptr, dptr, p, n, err);
+      if (vec > 1 && idx32)
+        NT_IDX_LAUNCH(scatter_kernel, iptr, dptr, true, V);
+      else if (vec > 1)
+        NT_IDX_LAUNCH(scatter_kernel, iptr, dptr, false, V);
+      else if (idx32)
+        NT_IDX_LAUNCH(scatter_kernel, iptr, dptr, true, 1);
       else
-        scatter_kernel<T, false><<<dim3(unsigned(blocks)), 256, 0, st>>>(
-            iptr, dptr, p, n, err);
+        NT_IDX_LAUNCH(scatter_kernel, iptr, dptr, false, 1);
     } else {
-      if (idx32)
-        gather_kernel<T, true><<<dim3(unsigned(blocks)), 256, 0, st>>>(
-            dptr, iptr, p, n, err);
+      if (vec > 1 && idx32)
+        NT_IDX_LAUNCH(gather_kernel, dptr, iptr, true, V);
+      else if (vec > 1)
+        NT_IDX_LAUNCH(gather_kernel, dptr, iptr, false, V);
+      else if (idx32)
+        NT_IDX_LAUNCH(gather_kernel, dptr, iptr, true, 1);
       else
-        gather_kernel<T, false><<<dim3(unsigned(blocks)), 256, 0, st>>>(
-            dptr, iptr, p, n, err);
+        NT_IDX_LAUNCH(gather_kernel, dptr, iptr, false, 1);
     }
+#undef NT_IDX_LAUNCH
   });
-  const hipError_t le = hipGetLastError();
-  int herr = 0;
-  const hipError_t ce =
-      le == hipSuccess
-          ? hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, st)
-          : le;
-  const hipError_t se = ce == hipSuccess ? hipStreamSynchronize(st) : ce;
-  NT_HIP_CHECK(se);
-  if (herr)
-    fail(NT_ERR_INDEX, "index out of range for its axis");
+  NT_LAUNCH_CHECK();
 }
 
 } // namespace

@@ -31,6 +31,12 @@ struct Error : std::exception {
 void set_last_error(const std::string &msg);
 void ensure_init();
 hipStream_t stream();
+// Device pointer to the deferred-error word: a kernel that finds an invalid
+// argument it cannot report synchronously stores an nt_status there (plain
+// store; any writer's value wins).  nt_sync and the device-to-host copy,
+// which synchronise anyway, raise it once and clear it.
+int *deferred_error_word();
+void raise_deferred_error();
 int device_cu_count();
 // Library-internal scratch allocations through the caching allocator.
 void *device_alloc(size_t nbytes);

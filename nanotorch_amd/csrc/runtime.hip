@@ -23,6 +23,10 @@ struct Runtime {
   bool available = false;
   int cu_count = 0;
   hipStream_t stream = nullptr;
+  // Deferred device-side error word: pinned, coherent host memory that
+  // kernels may store an nt_status into; read after stream syncs.
+  volatile int *deferred_host = nullptr;
+  int *deferred_dev = nullptr;
 };
 
 Runtime &rt() {
@@ -160,6 +164,13 @@ void ensure_init() {
   r.cu_count = prop.multiProcessorCount;
   // Default priority, non-blocking w.r.t. the legacy null stream.
   NT_HIP_CHECK(hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking));
+  void *word = nullptr;
+  NT_HIP_CHECK(hipHostMalloc(&word, sizeof(int), hipHostMallocCoherent));
+  *static_cast<volatile int *>(word) = 0;
+  void *dword = nullptr;
+  NT_HIP_CHECK(hipHostGetDevicePointer(&dword, word, 0));
+  r.deferred_host = static_cast<volatile int *>(word);
+  r.deferred_dev = static_cast<int *>(dword);
   r.available = true;
   r.initialised = true;
 }
@@ -173,6 +184,17 @@ bool ew_nontemporal() {
 }
 
 hipStream_t stream() { return rt().stream; }
+int *deferred_error_word() { return rt().deferred_dev; }
+
+void raise_deferred_error() {
+  volatile int *w = rt().deferred_host;
+  if (w == nullptr || *w == NT_OK)
+    return;
+  const int code = *w;
+  *w = NT_OK;
+  fail(code, "an earlier gather/scatter call met an index outside its axis "
+             "(found by the device-side check; those elements were skipped)");
+}
 int device_cu_count() { return rt().cu_count; }
 void *device_alloc(size_t nbytes) { return allocator().alloc(nbytes); }
 void device_free(void *p) { allocator().free(p); }
@@ -239,7 +261,10 @@ int nt_is_available(int *available) {
 }
 
 int nt_sync(void) {
-  return guard([] { NT_HIP_CHECK(hipStreamSynchronize(stream())); });
+  return guard([] {
+    NT_HIP_CHECK(hipStreamSynchronize(stream()));
+    raise_deferred_error();
+  });
 }
 
 const char *nt_last_error(void) { return g_last_error.c_str(); }
@@ -290,6 +315,7 @@ int nt_memcpy_d2h(void *dst, const void *src, size_t nbytes) {
     NT_HIP_CHECK(
         hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, stream()));
     NT_HIP_CHECK(hipStreamSynchronize(stream()));
+    raise_deferred_error();
   });
 }
 

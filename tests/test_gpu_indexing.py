@@ -129,10 +129,40 @@ def test_setitem_from_transposed_value(gpu):
 
 def test_out_of_range_index_through_abi(gpu):
     """A caller that skips the host checks gets IndexError from the kernel's
-    own bounds test, and no element outside the view is read."""
+    own bounds test at the next synchronisation, once; no element outside
+    the view is read (the gather writes zeros there) or written."""
     x = dev(np.arange(12, dtype=np.float32).reshape(3, 4))
     plan = _fancy.compute_plan((3, 4), ([0, 1],))
     plan.index_arrays = [np.array([0, 3], dtype=np.int64)]  # 3 >= axis length
-    out = nt.Tensor(np.zeros((2, 4), dtype=np.float32), device="cuda")
+    out = nt.Tensor(np.full((2, 4), 7.0, dtype=np.float32), device="cuda")
+    _fancy._device_call("nt_gather_axes", plan, x, out)  # queues only
     with pytest.raises(IndexError):
-        _fancy._device_call("nt_gather_axes", plan, x, out)
+        nt.sync()
+    nt.sync()  # reported once
+    assert out.cpu().tolist() == [[0.0, 1.0, 2.0, 3.0], [0.0] * 4]
+    # scatter: the bad row is skipped, the good one written
+    src = dev(np.full((2, 4), -1.0, dtype=np.float32))
+    _fancy._device_call("nt_scatter_axes", plan, src, x)
+    with pytest.raises(IndexError):
+        x.cpu()  # the device-to-host copy reports it too
+    assert x.cpu().tolist() == [[-1.0] * 4, [4.0, 5.0, 6.0, 7.0], [8.0, 9.0, 10.0, 11.0]]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.int64, np.bool_])
+def test_row_gather_scatter_vector_path(gpu, dtype):
+    """Row gathers / scatters take the 16-byte vector path when the rows are
+    contiguous and aligned; offset views and odd widths take the scalar
+    one.  Both against numpy, bit-exact."""
+    r = rng(6)
+    for rows_, width, off in ((300, 64, 0), (300, 64, 16), (300, 66, 0), (257, 48, 3)):
+        base = (r.standard_normal(rows_ * width + off) * 10).astype(dtype)
+        table = base[off:].reshape(rows_, width)
+        t = dev(base)[off:].reshape(rows_, width)
+        ids = r.integers(-rows_, rows_, (37,))
+        assert_bitexact(t[ids.tolist()].numpy(), table[ids], f"gather {width} {off}")
+        uniq = r.permutation(rows_)[:25]
+        vals = (r.standard_normal((25, width)) * 10).astype(dtype)
+        t[uniq.tolist()] = dev(vals)
+        want = table.copy()
+        want[uniq] = vals
+        assert_bitexact(t.numpy(), want, f"scatter {width} {off}")
