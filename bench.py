@@ -350,7 +350,7 @@ def _index_args(fn: str, plan, first, second, keep_alive: list) -> list:
     return args
 
 
-def bench_next(iters: int = 10) -> dict:
+def bench_next(iters: int = 12) -> dict:
     """The rows next to the hot path, each timed per launch with HIP events
     on the library stream: device casts and a comparison (no host round
     trip), strided copy of a transposed view, a batched matmul on the MFMA
@@ -358,54 +358,70 @@ def bench_next(iters: int = 10) -> dict:
     algorithmic (every operand once); GB/s against the HBM peak, TFLOP/s
     against the fp32 MFMA peak."""
     from nanotorch_amd import _fancy
+    import ctypes
     r = np.random.default_rng(6)
-    # [8192, 8192]: every case's operands exceed the 256 MB Infinity Cache,
-    # so back-to-back launches still stream from HBM
+    # [8192, 8192] operands in SETS copies used in turn: consecutive launches
+    # touch different buffers, several GB apart, so nothing is served from
+    # the 256 MB Infinity Cache (re-writing one output buffer back to back
+    # was measured ~20% faster than HBM allows).
+    SETS = 3
     shape = (8192, 8192)
     n = shape[0] * shape[1]
-    a = dev(r.standard_normal(shape).astype(np.float32))
-    b = dev(r.standard_normal(shape).astype(np.float32))
-    a64 = dev(r.standard_normal(shape))
-    lab = dev(r.integers(0, 1000, shape, dtype=np.int64))
-    o32, o64, ob = _fresh(shape), _fresh(shape, nt.float64), _fresh(shape, nt.bool_)
+
+    def copies(t):
+        out = [t]
+        for _ in range(SETS - 1):
+            c = _fresh(t.shape, t.dtype)
+            K.copy_view(t, c)
+            out.append(c)
+        return out
+
+    a = copies(dev(r.standard_normal(shape).astype(np.float32)))
+    b = copies(dev(r.standard_normal(shape).astype(np.float32)))
+    a64 = copies(dev(r.standard_normal(shape)))
+    lab = copies(dev(r.integers(0, 1000, shape, dtype=np.int64)))
+    o32 = [_fresh(shape) for _ in range(SETS)]
+    o64 = [_fresh(shape, nt.float64) for _ in range(SETS)]
+    ob = [_fresh(shape, nt.bool_) for _ in range(SETS)]
     B, Mb = 16, 1024
     xb = dev(r.standard_normal((B, Mb, Mb)).astype(np.float32))
     yb = dev((r.standard_normal((B, Mb, Mb)) / np.sqrt(Mb)).astype(np.float32))
     ob3 = _fresh((B, Mb, Mb))
     rows, width = 50000, 1024
-    table = dev(r.standard_normal((rows, width)).astype(np.float32))
+    tables = copies(dev(r.standard_normal((rows, width)).astype(np.float32)))
     ids = r.permutation(rows)[:8192]
-    gplan = _fancy.compute_plan(table.shape, (ids.tolist(),))
-    gout = _fresh(gplan.new_shape)
+    gplan = _fancy.compute_plan(tables[0].shape, (ids.tolist(),))
+    gouts = [_fresh(gplan.new_shape) for _ in range(SETS)]
     keep: list = []
-    gargs = _index_args("nt_gather_axes", gplan, table, gout, keep)
-    sargs = _index_args("nt_scatter_axes", gplan, gout, table, keep)
-    import ctypes
-    vab, vbb, vob = view(a), view(b), view(ob)
-    cmp_args = (_lib.GT, ctypes.byref(vab), ctypes.byref(vbb), ctypes.byref(vob))
+    gargs = [_index_args("nt_gather_axes", gplan, tables[k], gouts[k], keep) for k in range(SETS)]
+    sargs = [_index_args("nt_scatter_axes", gplan, gouts[k], tables[k], keep) for k in range(SETS)]
+    vws = [(view(a[k]), view(b[k]), view(ob[k])) for k in range(SETS)]
+    keep.append(vws)
+    cmp_args = [(_lib.GT, ctypes.byref(x), ctypes.byref(y), ctypes.byref(z)) for x, y, z in vws]
+    gbytes = 2 * gouts[0].numel * 4 + 8 * len(ids)
     cases = {
-        # name: (launch, bytes or None, flop or None)
-        "cast|f32->f64": (lambda: K.copy_view(a, o64), 12 * n, None),
-        "cast|f64->f32": (lambda: K.copy_view(a64, o32), 12 * n, None),
-        "cast|i64->f32": (lambda: K.copy_view(lab, o32), 12 * n, None),
-        "compare|gt": (lambda: _lib.call("nt_binary", *cmp_args), 9 * n, None),
-        "copy|transposed": (lambda: K.copy_view(a.T, o32), 8 * n, None),
-        "matmul|batched 16x1024^3": (lambda: K.matmul_into(xb, yb, ob3, accumulate=False),
+        # name: (launch of set k, bytes or None, flop or None)
+        "cast|f32->f64": (lambda k: K.copy_view(a[k], o64[k]), 12 * n, None),
+        "cast|f64->f32": (lambda k: K.copy_view(a64[k], o32[k]), 12 * n, None),
+        "cast|i64->f32": (lambda k: K.copy_view(lab[k], o32[k]), 12 * n, None),
+        "compare|gt": (lambda k: _lib.call("nt_binary", *cmp_args[k]), 9 * n, None),
+        "copy|transposed": (lambda k: K.copy_view(a[k].T, o32[k]), 8 * n, None),
+        "matmul|batched 16x1024^3": (lambda k: K.matmul_into(xb, yb, ob3, accumulate=False),
                                      None, 2 * B * Mb**3),
-        "gather|8192 rows of [50000,1024]": (lambda: _lib.call("nt_gather_axes", *gargs),
-                                             2 * gout.numel * 4 + 8 * len(ids), None),
-        "scatter|8192 rows of [50000,1024]": (lambda: _lib.call("nt_scatter_axes", *sargs),
-                                              2 * gout.numel * 4 + 8 * len(ids), None),
+        "gather|8192 rows of [50000,1024]": (lambda k: _lib.call("nt_gather_axes", *gargs[k]),
+                                             gbytes, None),
+        "scatter|8192 rows of [50000,1024]": (lambda k: _lib.call("nt_scatter_axes", *sargs[k]),
+                                              gbytes, None),
     }
     out = {}
     for name, (fn, nbytes, flop) in cases.items():
         # back-to-back launches of one case between two events: the average
         # launch, with the stream kept busy
-        fn()
+        fn(SETS - 1)
         e0, e1 = _lib.Event(), _lib.Event()
         e0.record()
-        for _ in range(iters):
-            fn()
+        for it in range(iters):
+            fn(it % SETS)
         e1.record()
         nt.sync()
         avg = e0.elapsed_ms(e1) / iters

@@ -26,6 +26,11 @@
 namespace nt {
 
 constexpr int IDX_MAX_FANCY = NT_MAX_DIMS;
+// Workgroups per CU of the grid-stride gather / scatter (32 measured 4%
+// faster than 16 on a row gather; 64 no faster).
+#ifndef NT_IDX_WG_PER_CU
+#define NT_IDX_WG_PER_CU 32
+#endif
 
 struct IndexPlan {
   int out_ndim;    // dims of the iteration space (gather: out, scatter: src)
@@ -296,7 +301,7 @@ void run_index(const nt_view *data, const nt_view *iter, const IndexPlan &base) 
     const int vec = index_vec<T>(data, iter, p);
     const int64_t groups = n / vec;
     const dim3 grid{unsigned(std::min<int64_t>((groups + 255) / 256,
-                                               int64_t(device_cu_count()) * 16)),
+                                               int64_t(device_cu_count()) * NT_IDX_WG_PER_CU)),
                     1u, 1u};
     constexpr int V = ew_vec<T>();
 #define NT_IDX_LAUNCH(K, A, B, I32, VV)                                        \
