@@ -76,6 +76,8 @@ class Tensor:
         storage, shape, out_dtype = None, None, None
         if hasattr(data, "__array__") and hasattr(data, "tolist"):
             storage, shape, out_dtype = _from_array_like(data, dtype, device)
+            if storage is None:
+                data = data.tolist()
         if storage is None:
             out_dtype, shape, storage = _extract_tensor_data(data, device, dtype)
         self._storage = storage
@@ -491,8 +493,9 @@ def _from_array_like(data, user_dtype, device):
         import numpy as np
     except ImportError:
         return None, None, None
+    shape = tuple(np.shape(data))  # ascontiguousarray makes a 0-d array 1-d
     arr = np.ascontiguousarray(data)
-    return Storage.from_buffer(arr, dt, device), tuple(arr.shape), dt
+    return Storage.from_buffer(arr, dt, device), shape, dt
 
 
 def _infer_strides(shape: TensorShape) -> TensorShape:
