@@ -412,6 +412,10 @@ def bench_next(iters: int = 12) -> dict:
                                              gbytes, None),
         "scatter|8192 rows of [50000,1024]": (lambda k: _lib.call("nt_scatter_axes", *sargs[k]),
                                               gbytes, None),
+        # the reference's generator stream drawn on the device: bytes written
+        "uniform|f32 [8192,8192]": (lambda k: _lib.call("nt_device_uniform", o32[k]._storage.data_ptr(),
+                                                        int(nt.float32), n, 0.0, 1.0),
+                                    4 * n, None),
     }
     out = {}
     for name, (fn, nbytes, flop) in cases.items():
@@ -433,6 +437,13 @@ def bench_next(iters: int = 12) -> dict:
             gbs = nbytes / (avg * 1e-3) / 1e9
             out[name] = {"ms": round(avg, 5), "GB/s": round(gbs, 1),
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    out["uniform|f32 [8192,8192]"]["Gdraws/s"] = round(n / (out["uniform|f32 [8192,8192]"]["ms"] * 1e-3) / 1e9, 2)
+    # the same stream on one host core (the reference draws it there)
+    hn = 1 << 24
+    hbuf = np.empty(hn, np.float32)
+    t0 = time.perf_counter()
+    _lib.call("nt_host_uniform", hbuf.ctypes.data, int(nt.float32), hn, 0.0, 1.0)
+    out["uniform|f32 host, 1 core"] = {"Gdraws/s": round(hn / (time.perf_counter() - t0) / 1e9, 3)}
     return out
 
 

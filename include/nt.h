@@ -283,12 +283,20 @@ int nt_scatter_axes(const nt_view *src, const nt_view *out, int32_t nfancy,
 /* ------------------------------------------------------------- host utils */
 
 /* Replaces `manual_seed` / `uniform` (src/cpp/random.h:5-13,
- * src/cpp/factory.cu:73-83): a 64-bit Mersenne Twister with libstdc++'s
- * uniform_real_distribution / uniform_int_distribution semantics, writing
- * into HOST memory. */
+ * src/cpp/factory.cu:73-83): the reference's one global std::mt19937_64
+ * (seeded from std::random_device until nt_manual_seed) drawn through
+ * libstdc++'s uniform_real_distribution<T>(low, high), T = float32 or
+ * float64.  nt_host_uniform writes n draws into HOST memory (no device is
+ * needed unless earlier draws ran there).  nt_device_uniform writes the same
+ * n draws -- the same stream, bit for bit -- into DEVICE memory, generated on
+ * the device and queued on the library stream; draws from either continue
+ * the one stream in call order.  The first device draw of a process builds
+ * the generator's jump tables on the host (a few hundred milliseconds). */
 int nt_manual_seed(uint64_t seed);
 int nt_host_uniform(void *host_out, int32_t dtype, int64_t n, double low,
                     double high);
+int nt_device_uniform(void *device_out, int32_t dtype, int64_t n, double low,
+                      double high);
 
 /* Timing events on the library stream (no reference counterpart; used by the
  * benchmark to time kernels on the stream they run on).  Timing-only events:

@@ -1,14 +1,13 @@
 // Device runtime of libnt: initialisation, the library stream, the caching
-// allocator, host<->device copies, fills, timing events and the host RNG.
+// allocator, host<->device copies, fills and timing events.
 //
 // Reference counterparts: src/cpp/cuda.{h,cpp} (availability, sync, error
 // checks), src/cpp/allocator.{h,cpp} (caching allocator), src/cpp/storage.cpp
-// (allocate/to/clone), src/cpp/factory.cu (fills) and src/cpp/random.h (RNG).
+// (allocate/to/clone) and src/cpp/factory.cu (fills).
 #include <algorithm>
 #include <cstdlib>
 #include <map>
 #include <mutex>
-#include <random>
 
 #include "ew_engine.h"
 
@@ -114,11 +113,6 @@ struct CachingAllocator {
 CachingAllocator &allocator() {
   static CachingAllocator a;
   return a;
-}
-
-std::mt19937_64 &host_rng() {
-  static std::mt19937_64 rng{std::random_device{}()};
-  return rng;
 }
 
 __global__ void fill_kernel_bytes(uint8_t *p, int64_t nbytes_pattern_units,
@@ -381,40 +375,6 @@ int nt_fill(void *data, int32_t dtype, int64_t n, double value) {
       NT_LAUNCH_CHECK();
     }
   });
-}
-
-int nt_manual_seed(uint64_t seed) {
-  try {
-    host_rng().seed(seed);
-  } catch (...) {
-    return NT_ERR_RUNTIME;
-  }
-  return NT_OK;
-}
-
-int nt_host_uniform(void *host_out, int32_t dtype, int64_t n, double low,
-                    double high) {
-  // No device needed: this is the reference's host-side generator.
-  try {
-    if (dtype == NT_FLOAT32) {
-      std::uniform_real_distribution<float> dist{float(low), float(high)};
-      float *o = static_cast<float *>(host_out);
-      for (int64_t i = 0; i < n; ++i)
-        o[i] = dist(host_rng());
-    } else if (dtype == NT_FLOAT64) {
-      std::uniform_real_distribution<double> dist{low, high};
-      double *o = static_cast<double *>(host_out);
-      for (int64_t i = 0; i < n; ++i)
-        o[i] = dist(host_rng());
-    } else {
-      set_last_error("nt_host_uniform: float dtype required");
-      return NT_ERR_VALUE;
-    }
-  } catch (const std::exception &e) {
-    set_last_error(e.what());
-    return NT_ERR_RUNTIME;
-  }
-  return NT_OK;
 }
 
 int nt_event_create(void **ev) {

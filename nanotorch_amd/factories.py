@@ -61,11 +61,19 @@ def arange(n: int, start: int = 0, step: int = 1, dtype: Dtype = dt.int64,
 
 
 def manual_seed(seed: int) -> None:
-    """Seeds the host generator behind rand / randint."""
+    """Seeds the one generator behind rand / randint (host and device draws
+    continue the same stream)."""
     _lib.call("nt_manual_seed", int(seed) & (2**64 - 1))
 
 
-def _host_uniform(n: int, dtype: Dtype) -> Storage:
+def _uniform(n: int, dtype: Dtype, device: Device) -> Storage:
+    """n draws of U[0, 1) in the reference's stream (factory.cu:73-83): on the
+    device they are generated there, on the host written to host memory."""
+    if device == Device.Cuda:
+        st = Storage.allocate(n, dtype, Device.Cuda)
+        if n:
+            _lib.call("nt_device_uniform", st.data_ptr(), int(dtype), n, 0.0, 1.0)
+        return st
     host = Storage(n, dtype, Device.Cpu)
     if n:
         _lib.call("nt_host_uniform", ctypes.addressof(host.host_array()), int(dtype), n,
@@ -75,23 +83,30 @@ def _host_uniform(n: int, dtype: Dtype) -> Storage:
 
 def rand(*shape: int, dtype: Dtype = dt.float32, requires_grad: bool = False,
          device: Device | DeviceLiteral = Device.Cpu) -> Tensor:
-    """U[0, 1) from a 64-bit Mersenne Twister, drawn on the host."""
+    """U[0, 1) from the reference's 64-bit Mersenne Twister stream."""
     if dtype <= dt.int64:
         raise ValueError("rand() cannot output non-float values.")
-    st = _host_uniform(math.prod(shape), dtype).to(get_std_device(device))
+    st = _uniform(math.prod(shape), dtype, get_std_device(device))
     return _factory(shape, st, requires_grad)
 
 
 def randint(low: int, high: int, shape: tuple[int, ...] | None = None,
             dtype: Dtype = dt.int64, requires_grad: bool = False,
             device: Device | DeviceLiteral = Device.Cpu) -> Tensor:
-    """floor-towards-zero of U[0,1) * (high - low) + low, computed in float32
-    as the reference does."""
+    """trunc(U[0,1) * (high - low) + low) in float32, then int64, then dtype:
+    the reference's composition (factories.py:241-253)."""
     if dtype == dt.bool_:
         raise ValueError("randint() cannot output bool values.")
     shp = () if shape is None else tuple(shape)
     n = math.prod(shp)
-    u = _host_uniform(n, dt.float32)
+    device = get_std_device(device)
+    if device == Device.Cuda:
+        u = _factory(shp, _uniform(n, dt.float32, device), False)
+        x = (u * (high - low) + low).to(dt.int64).to(dtype)
+        if requires_grad:
+            x.enable_grad()
+        return x
+    u = _uniform(n, dt.float32, device)
     # float32 arithmetic as in the reference: (u * f32(high - low)) + f32(low)
     f = ctypes.c_float
     span, lo = f(float(high - low)).value, f(float(low)).value

@@ -13,6 +13,10 @@
 //             sequential loop), :183-233 (keep/drop views)
 //   matmul    src/cpp/ops/matmul.cu:21-57 (sequential k dot product)
 //   unravel   src/cpp/tensor_view.cuh:42-52
+//   uniform   src/cpp/factory.cu:73-83 with src/cpp/random.h:5-13: one
+//             std::mt19937_64 drawn through std::uniform_real_distribution<T>
+//             element by element (the standard library of this compiler,
+//             libstdc++, is the reference's dependency for this path)
 // The logical index walks row-major order; outputs are contiguous.
 // Built with -O3 -ffp-contract=off and no fast-math, so each + - * / is one
 // IEEE rounding as in the reference, and the std:: math calls resolve to the
@@ -24,6 +28,7 @@
 #include <cstdint>
 #include <cstring>
 #include <limits>
+#include <random>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -431,6 +436,36 @@ int or_matmul(const or_view *a, const or_view *b, void *out) {
 
 int or_matmul_omp(const or_view *a, const or_view *b, void *out) {
   return matmul_impl(a, b, out, true);
+}
+
+// n draws of uniform_real_distribution<T>(low, high) from a std::mt19937_64
+// seeded with `seed`, after dropping the first `skip` engine outputs (one
+// draw consumes one output for float and double).
+int or_uniform(uint64_t seed, int64_t skip, int64_t n, int32_t dtype,
+               double low, double high, void *out) {
+  return guard([&] {
+    std::mt19937_64 eng(seed);
+    eng.discard((unsigned long long)skip);
+    if (dtype == 3) {
+      std::uniform_real_distribution<float> dist{float(low), float(high)};
+      for (int64_t i = 0; i < n; ++i)
+        static_cast<float *>(out)[i] = dist(eng);
+    } else if (dtype == 4) {
+      std::uniform_real_distribution<double> dist{low, high};
+      for (int64_t i = 0; i < n; ++i)
+        static_cast<double *>(out)[i] = dist(eng);
+    } else {
+      throw std::invalid_argument("or_uniform: float dtype required");
+    }
+  });
+}
+
+// The k-th (1-based) raw output of std::mt19937_64 seeded with `seed`.
+uint64_t or_mt64_output(uint64_t seed, int64_t k) {
+  std::mt19937_64 eng(seed);
+  if (k > 1)
+    eng.discard((unsigned long long)(k - 1));
+  return eng();
 }
 
 } // extern "C"

@@ -76,6 +76,11 @@ def lib():
         ]
         L.or_matmul.argtypes = [P, P, ctypes.c_void_p]
         L.or_matmul_omp.argtypes = [P, P, ctypes.c_void_p]
+        L.or_uniform.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64,
+                                 ctypes.c_int32, ctypes.c_double, ctypes.c_double,
+                                 ctypes.c_void_p]
+        L.or_mt64_output.argtypes = [ctypes.c_uint64, ctypes.c_int64]
+        L.or_mt64_output.restype = ctypes.c_uint64
         L.or_last_error.restype = ctypes.c_char_p
         _lib = L
     return _lib
@@ -163,6 +168,22 @@ def matmul(a: np.ndarray, b: np.ndarray, parallel: bool = False) -> np.ndarray:
     fn = lib().or_matmul_omp if parallel else lib().or_matmul
     _check(fn(ctypes.byref(va), ctypes.byref(vb), _out_ptr(out)))
     return out
+
+
+def uniform(seed: int, n: int, dtype=np.float32, skip: int = 0, low: float = 0.0,
+            high: float = 1.0) -> np.ndarray:
+    """Draws skip .. skip+n-1 of the reference's generator after
+    manual_seed(seed): std::mt19937_64 through
+    std::uniform_real_distribution<T>(low, high) (factory.cu:73-83)."""
+    out = np.empty(n, dtype=dtype)
+    code = _CODES[np.dtype(dtype)]
+    _check(lib().or_uniform(seed, skip, n, code, low, high, _out_ptr(out)))
+    return out
+
+
+def mt64_output(seed: int, k: int) -> int:
+    """The k-th (1-based) raw output of std::mt19937_64 seeded with seed."""
+    return int(lib().or_mt64_output(seed, k))
 
 
 # ------------------------------------------------- scalars as the reference

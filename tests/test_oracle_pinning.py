@@ -386,3 +386,27 @@ def test_rng_known_answer():
     assert buf[0] == np.float32(KA["rng"]["first"])
     # MSVC's value differs by one ulp (libstdc++ vs MSVC STL)
     assert abs(buf[1] - KA["rng"]["second_msvc"]) <= 2 * np.spacing(np.float32(0.64))
+
+
+def test_rng_oracle_pinned():
+    """The oracle's generator (std::mt19937_64 through
+    uniform_real_distribution) against what fixes it independently: the C++
+    standard's required 10000th output of a default-seeded mt19937_64
+    ([rand.predef]), the reference test-suite's known answer, and the closed
+    form of libstdc++'s generate_canonical for a 64-bit engine (one output u,
+    T(u) / 2^64 rounded to nearest, the largest T below 1 if that is 1)."""
+    assert O.mt64_output(5489, 10000) == 9981545732273789042
+    assert O.uniform(KA["rng"]["seed"], 1)[0] == np.float32(KA["rng"]["first"])
+    for seed in (0, 42, 2**64 - 1):
+        for k in (1, 2, 312, 313, 624, 10000):
+            u = np.array([O.mt64_output(seed, k)], dtype=np.uint64)
+            for dt, below_one in ((np.float32, np.float32(1) - np.float32(2.0**-24)),
+                                  (np.float64, 1.0 - 2.0**-53)):
+                want = u.astype(dt) * dt(2.0**-64)
+                want = np.where(want >= 1, dt(below_one), want)
+                got = O.uniform(seed, 1, dtype=dt, skip=k - 1)
+                assert got.tobytes() == want.astype(dt).tobytes(), (seed, k, dt)
+    # (b - a) * canonical + a, in T
+    lo, hi = np.float32(-2.5), np.float32(7.0)
+    base = O.uniform(9, 50)
+    assert O.uniform(9, 50, low=-2.5, high=7.0).tobytes() == (base * (hi - lo) + lo).tobytes()
