@@ -19,9 +19,12 @@
 // correlation of the 20280 raw words that follow the base with the bits of
 // g.  A call cuts its draws into substreams of SUB_WORDS raw words; the
 // start window of substream w is the base jumped by w * SUB_WORDS, from a
-// table g_w = x^(w SUB_WORDS) mod P built once per process on the host.  One
-// wave then runs each substream's recurrence 156 words (half a block) per
-// step, with the words of a half-block spread over its lanes.
+// table g_w = x^(w SUB_WORDS) mod P built once per process on the host.
+// Per launch round: one wave steps the 20280 raw words after the base
+// (rng_raw_kernel); one wave per (bit chunk, substream) correlates them
+// with g_w (rng_jump_kernel); one workgroup per substream runs its
+// recurrence half a block (156 words) per step in a producer wave and
+// tempers, converts and stores in consumer waves (rng_gen_kernel).
 #include <algorithm>
 #include <memory>
 #include <mutex>
@@ -92,21 +95,86 @@ void mt_twist(uint64_t *x) {
 
 // ------------------------------------------------------ device geometry
 
-constexpr int64_t SUB_WORDS = int64_t(MT_N) * 256; // raw words per substream
+constexpr int64_t SUB_WORDS = int64_t(MT_N) * 512; // raw words per substream
 constexpr int MAX_SUBSTREAMS = 512;                 // per launch round
 constexpr int POLY_WORDS = MT_N;                    // 19968 bits >= degree
 constexpr int JUMP_CHUNKS = 8;                      // bit ranges per jump
 constexpr int CHUNK_WORDS = POLY_WORDS / JUMP_CHUNKS; // 39
 constexpr int CHUNK_BITS = CHUNK_WORDS * 64;          // 2496
 constexpr int JUMP_SPAN = CHUNK_BITS + MT_N;          // raw words per chunk
+constexpr int JUMP_RUN = 6;                           // window words per lane
+constexpr int JUMP_LANES = MT_N / JUMP_RUN;           // 52
+constexpr int JUMP_WAVES = 4;                         // substreams per group
 constexpr int RAW_HALVES = 130;                       // half-blocks of raw
 constexpr int RAW_WORDS = RAW_HALVES * MT_M;          // 20280
+constexpr int GEN_BATCH = 16;    // half-blocks handed over per barrier
+constexpr int GEN_THREADS = 512; // one producer wave, seven consumer waves
 static_assert(CHUNK_WORDS * JUMP_CHUNKS == POLY_WORDS, "chunking");
 static_assert((JUMP_CHUNKS - 1) * CHUNK_BITS + JUMP_SPAN <= RAW_WORDS,
               "a jump chunk reads past the raw sequence");
+static_assert(JUMP_LANES * JUMP_RUN == MT_N && JUMP_LANES <= 64, "lanes");
+static_assert(CHUNK_BITS - 1 + JUMP_RUN + (JUMP_LANES - 1) * JUMP_RUN <
+                  JUMP_SPAN,
+              "a lane's register window stays inside the chunk's raw words");
 static_assert(SUB_WORDS % MT_N == 0, "substreams hold whole blocks");
+static_assert((GEN_BATCH * MT_M) % 2 == 0, "consumers read word pairs");
 
 // ------------------------------------------------------------- kernels
+
+// x_{k+312} from x_k, the low 32 bits of x_{k+1} (only its low 31 bits and
+// bit 0 enter) and x_{k+156}.
+__device__ inline uint64_t mt_next_lo(uint64_t xk, uint32_t xk1_lo,
+                                      uint64_t xkm) {
+  const uint64_t y = (xk & MT_UPPER) | (xk1_lo & MT_LOWER);
+  return xkm ^ (y >> 1) ^ ((xk1_lo & 1) ? MT_A : 0);
+}
+
+// Lane l receives v of lane (l + 1) mod 64: a DPP wavefront rotate.
+__device__ inline uint32_t from_next_lane(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x134 /*wave_rol:1*/,
+                                              0xf, 0xf, false));
+}
+
+constexpr int HB_LANES = MT_M / 3; // 52 lanes hold a half-block
+
+// A wave holding two consecutive half-blocks of the raw sequence: lane
+// l < 52 has words 3l, 3l+1, 3l+2 of each; lanes 52-63 hold zeros (and
+// stay zero: the recurrence maps zeros to zero).
+struct HalfBlocks {
+  uint64_t a[3], b[3]; // half-blocks t-2 and t-1
+  uint32_t nx;         // low half of word 3l+3 of a
+
+  __device__ void load(const uint64_t *win, int l) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      a[j] = l < HB_LANES ? win[3 * l + j] : 0;
+      b[j] = l < HB_LANES ? win[MT_M + 3 * l + j] : 0;
+    }
+    set_nx(l, from_next_lane(uint32_t(a[0])), b[0]);
+  }
+
+  // Word 3l+3 of a is the next lane's first word; for l = 51 it is word
+  // 156, b's first word, held by lane 0.
+  __device__ void set_nx(int l, uint32_t next_first, uint64_t b0) {
+    const uint32_t z = __builtin_amdgcn_readfirstlane(int(uint32_t(b0)));
+    nx = l == HB_LANES - 1 ? z : (l < HB_LANES - 1 ? next_first : 0u);
+  }
+
+  // Half-block t into c; then (a, b) = (b, c).  The lane exchange for the
+  // next step reads b, known before c.
+  __device__ void step(int l, uint64_t (&c)[3]) {
+    const uint32_t next_first = from_next_lane(uint32_t(b[0]));
+    c[0] = mt_next_lo(a[0], uint32_t(a[1]), b[0]);
+    c[1] = mt_next_lo(a[1], uint32_t(a[2]), b[1]);
+    c[2] = mt_next_lo(a[2], nx, b[2]);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      a[j] = b[j];
+      b[j] = c[j];
+    }
+    set_nx(l, next_first, b[0]);
+  }
+};
 
 // Draws 0 .. first-1 come from the current block (words p .. p+first-1);
 // next_block, when given, receives the following block (one twist).
@@ -131,83 +199,101 @@ __global__ __launch_bounds__(320) void rng_head_kernel(
     next_block[t] = nb[t];
 }
 
-// raw[0 .. RAW_WORDS) = the raw words from the base window on.  Half-block
-// t needs half-blocks t-1 and t-2 only: a ring of three in LDS.
-__global__ __launch_bounds__(256) void rng_raw_kernel(const uint64_t *base,
-                                                      uint64_t *raw) {
-  __shared__ uint64_t ring[3][MT_M];
-  const int i = threadIdx.x;
-  if (i < MT_M) {
-    ring[0][i] = raw[i] = base[i];
-    ring[1][i] = raw[MT_M + i] = base[MT_M + i];
-  }
-  __syncthreads();
-  for (int t = 2; t < RAW_HALVES; ++t) {
-    const uint64_t *a = ring[(t - 2) % 3];
-    const uint64_t *b = ring[(t - 1) % 3];
-    if (i < MT_M) {
-      const uint64_t v =
-          mt_next(a[i], i + 1 < MT_M ? a[i + 1] : b[0], b[i]);
-      ring[t % 3][i] = v;
-      raw[int64_t(t) * MT_M + i] = v;
+// raw[0 .. RAW_WORDS) = the raw words from the base window on: one wave
+// stepping half-blocks in registers.
+__global__ __launch_bounds__(64) void rng_raw_kernel(const uint64_t *base,
+                                                     uint64_t *raw) {
+  const int l = threadIdx.x;
+  HalfBlocks hb;
+  hb.load(base, l);
+  if (l < HB_LANES)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      raw[3 * l + j] = hb.a[j];
+      raw[MT_M + 3 * l + j] = hb.b[j];
     }
-    __syncthreads();
+  for (int t = 2; t < RAW_HALVES; ++t) {
+    uint64_t c[3];
+    hb.step(l, c);
+    if (l < HB_LANES)
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        raw[int64_t(t) * MT_M + 3 * l + j] = c[j];
   }
 }
 
 // partial[(w-1, c)][m] = XOR over the set bits i of g_w in chunk c of
-// raw[i + m]: chunk c's share of the start window of substream w.
-__global__ __launch_bounds__(320) void rng_jump_kernel(
-    const uint64_t *raw, const uint64_t *polys, uint64_t *partial) {
+// raw[i + m]: chunk c's share of the start window of substream w.  A
+// workgroup loads chunk c's raw words into LDS once for JUMP_WAVES
+// substreams, one wave each; lane l owns m = 6l .. 6l+5.  Per 32 bits of g
+// the lane loads the 38 words its six m's meet into registers, then each
+// set (wave-uniform) bit b costs six 64-bit XORs of registers b .. b+5.
+__global__ __launch_bounds__(64 * JUMP_WAVES) void rng_jump_kernel(
+    const uint64_t *raw, const uint64_t *polys, uint64_t *partial,
+    int jumps) {
   __shared__ uint64_t win[JUMP_SPAN];
   const int c = blockIdx.x;
-  const int w1 = blockIdx.y; // substream w = w1 + 1
+  const int l = threadIdx.x & 63;
+  const int w1 = blockIdx.y * JUMP_WAVES + (threadIdx.x >> 6); // w = w1 + 1
   const int64_t i0 = int64_t(c) * CHUNK_BITS;
-  for (int k = threadIdx.x; k < JUMP_SPAN; k += blockDim.x)
+  for (int k = threadIdx.x; k < JUMP_SPAN; k += 64 * JUMP_WAVES)
     win[k] = raw[i0 + k];
   __syncthreads();
-  const uint64_t *g = polys + int64_t(w1) * POLY_WORDS + c * CHUNK_WORDS;
-  const int m = threadIdx.x;
-  if (m < MT_N) {
-    uint64_t acc = 0;
-    for (int k = 0; k < CHUNK_WORDS; ++k) {
-      uint64_t bits = g[k];
-      while (bits) {
-        const int b = __builtin_ctzll(bits);
-        bits &= bits - 1;
-        acc ^= win[k * 64 + b + m];
+  if (w1 >= jumps)
+    return;
+  const int m0 = l < JUMP_LANES ? l * JUMP_RUN : 0;
+  const uint32_t *g = reinterpret_cast<const uint32_t *>(
+      polys + int64_t(w1) * POLY_WORDS + c * CHUNK_WORDS);
+  uint64_t acc[JUMP_RUN], w[32 + JUMP_RUN];
+#pragma unroll
+  for (int r = 0; r < JUMP_RUN; ++r) {
+    acc[r] = 0;
+    w[r] = win[m0 + r];
+  }
+  for (int k = 0; k < 2 * CHUNK_WORDS; ++k) {
+    // w[r] = word 32k + m0 + r; the last index read is
+    // 32 * 77 + 6 + 306 + 31 = JUMP_SPAN - 1
+#pragma unroll
+    for (int t = 0; t < 32; ++t)
+      w[JUMP_RUN + t] = win[k * 32 + JUMP_RUN + m0 + t];
+    const uint32_t bits = g[k]; // little-endian: bits 32k .. 32k+31
+#pragma unroll
+    for (int b = 0; b < 32; ++b)
+      if ((bits >> b) & 1) {
+#pragma unroll
+        for (int r = 0; r < JUMP_RUN; ++r)
+          acc[r] ^= w[b + r];
       }
-    }
-    partial[(int64_t(w1) * JUMP_CHUNKS + c) * MT_N + m] = acc;
+#pragma unroll
+    for (int r = 0; r < JUMP_RUN; ++r)
+      w[r] = w[32 + r];
+  }
+  if (l < JUMP_LANES) {
+    uint64_t *dst = partial + (int64_t(w1) * JUMP_CHUNKS + c) * MT_N + m0;
+#pragma unroll
+    for (int r = 0; r < JUMP_RUN; ++r)
+      dst[r] = acc[r];
   }
 }
 
-__device__ inline uint64_t shfl64(uint64_t v, int src) {
-  const int lo = __shfl(int(uint32_t(v)), src);
-  const int hi = __shfl(int(uint32_t(v >> 32)), src);
-  return (uint64_t(uint32_t(hi)) << 32) | uint32_t(lo);
-}
-
-__device__ inline uint64_t lane0_64(uint64_t v) {
-  const int lo = __builtin_amdgcn_readfirstlane(int(uint32_t(v)));
-  const int hi = __builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32)));
-  return (uint64_t(uint32_t(hi)) << 32) | uint32_t(lo);
-}
-
-// One wave per substream of one round.  Substream w covers raw words
+// One workgroup per substream of one round.  Substream w covers raw words
 // [w SUB_WORDS, w SUB_WORDS + count) of the round (count = min(SUB_WORDS,
 // round_words - w SUB_WORDS)) and writes their draws to out + w SUB_WORDS.
-// Lane l holds word l + 64 j of a half-block in slot j (slot 2 for l < 28).
-// The last wave also writes the block starting at local word final_lo to
-// final_words (the generator's new state), or, when next_base is given, the
-// window right after its range (the next round's base).
+// Wave 0 runs the recurrence in registers and hands GEN_BATCH half-blocks
+// per barrier to waves 1-7 through a double buffer in LDS; they temper,
+// convert and store.  The last workgroup's producer also writes the block
+// starting at local word final_lo to final_words (the generator's new
+// state), or, when next_base is given, the window right after its range
+// (the next round's base).
 template <class T>
-__global__ __launch_bounds__(64) void rng_gen_kernel(
+__global__ __launch_bounds__(GEN_THREADS) void rng_gen_kernel(
     const uint64_t *base, const uint64_t *partial, int64_t round_words,
     T *out, T lo, T span, uint64_t *final_words, int64_t final_lo,
     uint64_t *next_base) {
+  __shared__ __align__(16) uint64_t ring[2][GEN_BATCH * MT_M];
   const int w = blockIdx.x;
-  const int l = threadIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63;
   const bool last = w == int(gridDim.x) - 1;
   const int64_t count =
       round_words - int64_t(w) * SUB_WORDS < SUB_WORDS
@@ -218,66 +304,82 @@ __global__ __launch_bounds__(64) void rng_gen_kernel(
     end = final_lo + MT_N > end ? final_lo + MT_N : end;
   if (last && next_base)
     end = SUB_WORDS + MT_N;
+  const int64_t halves = (end + MT_M - 1) / MT_M;
+  const int64_t batches = (halves + GEN_BATCH - 1) / GEN_BATCH;
+  uint64_t *keep = last ? (final_words ? final_words : next_base) : nullptr;
+  const int64_t keep_lo = final_words ? final_lo : SUB_WORDS;
   T *o = out + int64_t(w) * SUB_WORDS;
 
-  uint64_t h0[3], h1[3];
+  HalfBlocks hb;
+  if (wave == 0) {
+    if (w == 0) {
+      hb.load(base, l);
+    } else {
+      const uint64_t *pp = partial + int64_t(w - 1) * JUMP_CHUNKS * MT_N;
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const int i = l + 64 * j;
-    h0[j] = h1[j] = 0;
-    if (i < MT_M) {
-      if (w == 0) {
-        h0[j] = base[i];
-        h1[j] = base[MT_M + i];
-      } else {
-        const uint64_t *pp =
-            partial + int64_t(w - 1) * JUMP_CHUNKS * MT_N;
-        for (int c = 0; c < JUMP_CHUNKS; ++c) {
-          h0[j] ^= pp[c * MT_N + i];
-          h1[j] ^= pp[c * MT_N + MT_M + i];
-        }
+      for (int j = 0; j < 3; ++j) {
+        hb.a[j] = hb.b[j] = 0;
+        if (l < HB_LANES)
+          for (int c = 0; c < JUMP_CHUNKS; ++c) {
+            hb.a[j] ^= pp[c * MT_N + 3 * l + j];
+            hb.b[j] ^= pp[c * MT_N + MT_M + 3 * l + j];
+          }
       }
+      hb.set_nx(l, from_next_lane(uint32_t(hb.a[0])), hb.b[0]);
     }
   }
 
-  auto emit = [&](const uint64_t (&h)[3], int64_t t) {
+  for (int64_t q = 0; q <= batches; ++q) {
+    if (wave == 0) {
+      if (q < batches) {
+        uint64_t *dst = ring[q & 1];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int i = l + 64 * j;
-      if (i >= MT_M)
-        continue;
-      const int64_t pos = t * MT_M + i;
-      if (pos < count)
-        o[pos] = uniform_of<T>(h[j], lo, span);
-      if (last && final_words && pos >= final_lo && pos < final_lo + MT_N)
-        final_words[pos - final_lo] = h[j];
-      if (last && next_base && pos >= SUB_WORDS && pos < SUB_WORDS + MT_N)
-        next_base[pos - SUB_WORDS] = h[j];
-    }
-  };
-
-  emit(h0, 0);
-  emit(h1, 1);
-  const int src = (l + 1) & 63;
-  for (int64_t t = 2; t * MT_M < end; ++t) {
-    // word i + 1 of half-block t-2: the next lane's word, the next slot's
-    // first word for lane 63, half-block t-1's first word for word 155.
-    const uint64_t s0 = shfl64(h0[0], src);
-    const uint64_t s1 = shfl64(h0[1], src);
-    const uint64_t s2 = shfl64(h0[2], src);
-    const uint64_t z1 = lane0_64(h0[1]);
-    const uint64_t z2 = lane0_64(h0[2]);
-    const uint64_t z3 = lane0_64(h1[0]);
-    uint64_t h2[3];
-    h2[0] = mt_next(h0[0], l == 63 ? z1 : s0, h1[0]);
-    h2[1] = mt_next(h0[1], l == 63 ? z2 : s1, h1[1]);
-    h2[2] = l < 28 ? mt_next(h0[2], l == 27 ? z3 : s2, h1[2]) : 0;
-    emit(h2, t);
+        for (int k = 0; k < GEN_BATCH; ++k) {
+          const int64_t t = q * GEN_BATCH + k;
+          uint64_t c[3];
+          if (t == 0) {
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      h0[j] = h1[j];
-      h1[j] = h2[j];
+            for (int j = 0; j < 3; ++j)
+              c[j] = hb.a[j];
+          } else if (t == 1) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+              c[j] = hb.b[j];
+          } else {
+            hb.step(l, c);
+          }
+          if (l < HB_LANES)
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+              dst[k * MT_M + 3 * l + j] = c[j];
+          if (keep && t * MT_M + MT_M > keep_lo && t * MT_M < keep_lo + MT_N &&
+              l < HB_LANES)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+              const int64_t at = t * MT_M + 3 * l + j - keep_lo;
+              if (at >= 0 && at < MT_N)
+                keep[at] = c[j];
+            }
+        }
+      }
+    } else if (q > 0) {
+      // two words per thread and pass (one 16-byte LDS read)
+      const ulonglong2 *src =
+          reinterpret_cast<const ulonglong2 *>(ring[(q - 1) & 1]);
+      const int64_t p0 = (q - 1) * GEN_BATCH * MT_M;
+      for (int j = threadIdx.x - 64; j < GEN_BATCH * MT_M / 2;
+           j += GEN_THREADS - 64) {
+        const ulonglong2 v = src[j];
+        const int64_t pos = p0 + 2 * j;
+        if (pos + 1 < count) {
+          o[pos] = uniform_of<T>(v.x, lo, span);
+          o[pos + 1] = uniform_of<T>(v.y, lo, span);
+        } else if (pos < count) {
+          o[pos] = uniform_of<T>(v.x, lo, span);
+        }
+      }
     }
+    __syncthreads();
   }
 }
 
@@ -461,13 +563,14 @@ void device_draws(Generator &g, T *out, int64_t n, T lo, T span) {
     uint64_t *base = d.base[r & 1];
     if (subs > 1) {
       ensure_polys(d, subs - 1);
-      rng_raw_kernel<<<1, 256, 0, s>>>(base, d.raw);
+      rng_raw_kernel<<<1, 64, 0, s>>>(base, d.raw);
       NT_LAUNCH_CHECK();
-      rng_jump_kernel<<<dim3(JUMP_CHUNKS, unsigned(subs - 1)), 320, 0, s>>>(
-          d.raw, d.polys, d.partial);
+      const unsigned groups = unsigned((subs - 1 + JUMP_WAVES - 1) / JUMP_WAVES);
+      rng_jump_kernel<<<dim3(JUMP_CHUNKS, groups), 64 * JUMP_WAVES, 0, s>>>(
+          d.raw, d.polys, d.partial, subs - 1);
       NT_LAUNCH_CHECK();
     }
-    rng_gen_kernel<T><<<unsigned(subs), 64, 0, s>>>(
+    rng_gen_kernel<T><<<unsigned(subs), GEN_THREADS, 0, s>>>(
         base, d.partial, words, out + first + done, lo, span,
         last ? d.words : nullptr, final_lo,
         last ? nullptr : d.base[(r + 1) & 1]);
