@@ -570,7 +570,7 @@ PROFILE_FILES = {
     "red": ("reduce_config3_trace.md", "Kernel statistics: config-3 reductions [8192, 8192] fp32"),
     "mm": ("matmul_config4_trace.md", "Kernel statistics: config-4 MatMulOp forward + dA + dB"),
     "mlp": ("mlp_config5_trace.md", "Kernel statistics: config-5 4-layer MLP training steps"),
-    "next": ("next_rows_trace.md", "Kernel statistics: casts, comparison, strided copy, "
+    "next": ("next_rows_trace.md", "Kernel statistics: casts, comparison, strided copy, device uniform draws, "
                                    "batched matmul, gather / scatter (the rows beside the path)"),
 }
 _UN = {0: "exp", 1: "log", 2: "neg", 3: "relu", 4: "sqrt", 5: "tanh", 6: "sigmoid", 7: "pow"}
@@ -579,8 +579,9 @@ _BI = {0: "add", 1: "sub", 2: "mul", 3: "truediv"}
 
 def _short(name: str) -> str:
     import re
-    n = re.sub(r"\(.*$", "", name)
-    return n.replace("void nt::", "").replace("nt::", "").replace("(anonymous namespace)::", "")
+    n = name.replace("(anonymous namespace)::", "")
+    n = re.sub(r"\(.*$", "", n)
+    return n.replace("void nt::", "").replace("nt::", "")
 
 
 def _sweep_key(name: str):

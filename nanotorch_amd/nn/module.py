@@ -103,6 +103,6 @@ def _kaiming_W(fan_in: int, fan_out: int, device: Device | str = "cuda") -> Tens
             f"Cannot initialize Linear with {fan_in=}, {fan_out=} (non-positive)."
         )
     z = math.sqrt(6 / fan_in)
-    u = rand(fan_in, fan_out).to("cuda")
+    u = rand(fan_in, fan_out, device="cuda")  # drawn on the device, same stream
     w = 2 * u * z - z
     return w if str(device) in ("cuda", "Device.Cuda") or device == Device.Cuda else w.to(device)
