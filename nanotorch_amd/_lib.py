@@ -90,6 +90,7 @@ _SIGNATURES = {
     "nt_manual_seed": (c_int, [c_uint64]),
     "nt_host_uniform": (c_int, [c_void_p, c_int32, c_int64, c_double, c_double]),
     "nt_device_uniform": (c_int, [c_void_p, c_int32, c_int64, c_double, c_double]),
+    "nt_rng_prepare": (c_int, []),
     "nt_event_create": (c_int, [POINTER(c_void_p)]),
     "nt_event_record": (c_int, [c_void_p]),
     "nt_event_elapsed_ms": (c_int, [c_void_p, c_void_p, POINTER(c_float)]),

@@ -486,11 +486,14 @@ void build_jump_base(JumpTables &jt) {
   jt.ready = true;
 }
 
-// Makes g_1 .. g_count available on the device.
-void ensure_polys(DeviceBuffers &d, int count) {
+JumpTables &jump_tables() {
   static JumpTables jt;
-  if (count <= d.polys_on_device)
-    return;
+  return jt;
+}
+
+// Host tables g_1 .. g_count (no device work).
+const JumpTables &host_polys(int count) {
+  JumpTables &jt = jump_tables();
   if (!jt.ready)
     build_jump_base(jt);
   while (jt.count < count) {
@@ -504,6 +507,14 @@ void ensure_polys(DeviceBuffers &d, int count) {
     jt.table.insert(jt.table.end(), g.begin(), g.end());
     ++jt.count;
   }
+  return jt;
+}
+
+// Makes g_1 .. g_count available on the device.
+void ensure_polys(DeviceBuffers &d, int count) {
+  if (count <= d.polys_on_device)
+    return;
+  const JumpTables &jt = host_polys(count);
   const int from = d.polys_on_device;
   NT_HIP_CHECK(hipMemcpy(d.polys + size_t(from) * POLY_WORDS,
                          jt.table.data() + size_t(from) * POLY_WORDS,
@@ -623,6 +634,22 @@ int nt_host_uniform(void *host_out, int32_t dtype, int64_t n, double low,
     } else {
       host_draws(g, static_cast<double *>(host_out), n, low, high - low);
     }
+  } catch (const Error &e) {
+    set_last_error(e.msg);
+    return e.code;
+  } catch (const std::exception &e) {
+    set_last_error(e.what());
+    return NT_ERR_RUNTIME;
+  }
+  return NT_OK;
+}
+
+int nt_rng_prepare(void) {
+  // Host only: the generator's polynomial, jump tables and their check.
+  try {
+    Generator &g = generator();
+    std::lock_guard<std::mutex> lock(g.mu);
+    host_polys(MAX_SUBSTREAMS - 1);
   } catch (const Error &e) {
     set_last_error(e.msg);
     return e.code;
