@@ -154,6 +154,7 @@ struct TileCoord {
   float *C;
 };
 
+template <int BM = MM_BM, int BN = MM_BN>
 __device__ __forceinline__ TileCoord mm_tile_coord(const MMArgs &g) {
   const int64_t per_batch = g.tiles_m * g.tiles_n;
   int64_t bid = blockIdx.x;
@@ -169,8 +170,8 @@ __device__ __forceinline__ TileCoord mm_tile_coord(const MMArgs &g) {
                                                        : GROUP;
   const int64_t in_group = tile - group * GROUP * g.tiles_n;
   TileCoord tc;
-  tc.m0 = (first_m + in_group % gsize) * MM_BM;
-  tc.n0 = (in_group / gsize) * MM_BN;
+  tc.m0 = (first_m + in_group % gsize) * BM;
+  tc.n0 = (in_group / gsize) * BN;
   tc.A = g.A;
   tc.B = g.B;
   tc.C = g.C;
@@ -434,6 +435,171 @@ __global__ __launch_bounds__(MM_THREADS, 2) void mm_f32_mfma_dl_kernel(
   mm_epilogue(g, tc, acc, wm, wn, h, li);
 }
 
+// ---------------------------------------- wide tile (direct-to-LDS, gfx950)
+
+// Workgroup tile 256x256, k-tile 32, 8 waves in a 2x4 grid (two per SIMD),
+// each wave owns a 128x64 block = 4x2 MFMA 32x32 blocks (128 accumulator
+// registers per lane).  Between two barriers a SIMD runs 256 MFMAs against
+// 128 in the 128x128 kernel, each A fragment read from LDS feeds two MFMAs
+// and each B fragment four, and every operand element crosses from L2 once
+// per 256 (not 128) outputs.  Two direct-loaded stages per operand take
+// 128 KB of LDS: one workgroup per CU.  Used for M and N multiples of 256
+// and K a multiple of 64 when the 256x256 tiles give every CU one.
+constexpr int WD_BM = 256, WD_BN = 256, WD_THREADS = 512;
+constexpr int WD_STAGE = WD_BM * MM_BK; // floats per operand stage (32 KB)
+
+// As DirectTile, for 256 rows of full tiles (no row is clamped): each of the
+// 4 instructions of a wave fills 1 KB of a stage:
+//   layout K : [256 mn][32 k], chunks swizzled (dl_swz); 8 rows each.
+//              Instruction j covers rows 32 wave + 8 j + lane / 8, whose
+//              swizzle is (lane / 8) ^ (j & 1): two per-lane bases, the
+//              rest uniform offsets.
+//   layout MN: [32 k][256 mn]; one k row each: one per-lane base.
+template <int LAY> struct WideDirectTile {
+  const float *base[2];
+  int64_t jstep; // elements between instruction j and j + 2 (K) / j + 1 (MN)
+  int64_t kstep; // elements between two k-tiles
+  __device__ __forceinline__ void init(const float *p, int64_t mn0,
+                                       int64_t s_mn, int64_t s_k, int wave,
+                                       int lane) {
+    if constexpr (LAY == LAY_K) {
+      const int64_t row = mn0 + wave * 32 + lane / 8;
+#pragma unroll
+      for (int par = 0; par < 2; ++par)
+        base[par] = p + (row + 8 * par) * s_mn +
+                    4 * ((lane % 8) ^ (lane / 8) ^ par);
+      jstep = 16 * s_mn;
+      kstep = 32;
+    } else {
+      base[0] = base[1] = p + int64_t(wave * 4) * s_k + mn0 + 4 * lane;
+      jstep = s_k;
+      kstep = 32 * s_k;
+    }
+  }
+  __device__ __forceinline__ void issue(float *stage, int64_t kt,
+                                        int wave) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float *src =
+          LAY == LAY_K ? base[j & 1] + (j / 2) * jstep + kt * kstep
+                       : base[0] + j * jstep + kt * kstep;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)src,
+          (__attribute__((address_space(3))) void *)(stage +
+                                                     (wave * 4 + j) * 256),
+          16, 0, 0);
+    }
+  }
+};
+
+// f[i][kk] = element (mn + 32 i, h * 16 + 8 * half + kk) of a wide stage.
+template <int LAY, int NB>
+__device__ __forceinline__ void wd_frags(const float *stage, int mn, int li,
+                                         int h, int half, float (&f)[NB][8]) {
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int row = mn + 32 * i + li;
+    if constexpr (LAY == LAY_K) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int pc = (4 * h + 2 * half + q) ^ dl_swz(row);
+        const float4 w =
+            *reinterpret_cast<const float4 *>(stage + row * 32 + pc * 4);
+        f[i][4 * q + 0] = w.x;
+        f[i][4 * q + 1] = w.y;
+        f[i][4 * q + 2] = w.z;
+        f[i][4 * q + 3] = w.w;
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        f[i][kk] = stage[(h * 16 + 8 * half + kk) * WD_BM + row];
+    }
+  }
+}
+
+// The k-tile in two halves of 8 MFMA steps: 48 fragment registers live.
+template <int LA, int LB>
+__device__ __forceinline__ void wd_compute(const float *sa, const float *sb,
+                                           int wm, int wn, int li, int h,
+                                           floatx16 (&acc)[4][2]) {
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    float fa[4][8], fb[2][8];
+    wd_frags<LA, 4>(sa, wm * 128, li, h, half, fa);
+    wd_frags<LB, 2>(sb, wn * 64, li, h, half, fb);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+              fa[i][kk], fb[j][kk], acc[i][j], 0, 0, 0);
+  }
+}
+
+template <int LA, int LB>
+__global__ __launch_bounds__(WD_THREADS, 1) void mm_f32_mfma_wide_kernel(
+    MMArgs g) {
+  __shared__ __align__(16) float sA0[WD_STAGE], sB0[WD_STAGE];
+  __shared__ __align__(16) float sA1[WD_STAGE], sB1[WD_STAGE];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int h = lane >> 5, li = lane & 31;
+  const TileCoord tc = mm_tile_coord<WD_BM, WD_BN>(g);
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc[i][j][r] = 0.f;
+
+  WideDirectTile<LA> ta;
+  WideDirectTile<LB> tb;
+  ta.init(tc.A, tc.m0, g.sAm, g.sAk, wave, lane);
+  tb.init(tc.B, tc.n0, g.sBn, g.sBk, wave, lane);
+  // K is a multiple of 64: k-tiles come in pairs, one per stage, and the
+  // loop has a single exit (an exit between the two stages made the
+  // compiler copy and spill the accumulators).
+  const int64_t ktiles = g.K / 32;
+  ta.issue(sA0, 0, wave);
+  tb.issue(sB0, 0, wave);
+  dl_wait_and_sync();
+  for (int64_t kt = 0; kt < ktiles; kt += 2) {
+    ta.issue(sA1, kt + 1, wave);
+    tb.issue(sB1, kt + 1, wave);
+    wd_compute<LA, LB>(sA0, sB0, wm, wn, li, h, acc);
+    dl_wait_and_sync();
+    if (kt + 2 < ktiles) {
+      ta.issue(sA0, kt + 2, wave);
+      tb.issue(sB0, kt + 2, wave);
+    }
+    wd_compute<LA, LB>(sA1, sB1, wm, wn, li, h, acc);
+    dl_wait_and_sync();
+  }
+
+  // lane holds column li of each 32x32 block, rows 8*(r/4) + 4*h + (r%4)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = tc.n0 + wn * 64 + j * 32 + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row =
+            tc.m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        float *dst = tc.C + row * g.sCm + col * g.sCn;
+        const float v = acc[i][j][r];
+        *dst = g.accumulate ? (*dst + v) : v;
+      }
+    }
+}
+
 // ------------------------------------------------ SIMT (non-fp32) kernel
 
 template <class T> struct MMArgsT {
@@ -490,6 +656,18 @@ namespace {
 template <int LA, int LB> void launch_mfma(const MMArgs &a, int64_t blocks) {
   if constexpr (LA != LAY_GEN && LB != LAY_GEN) {
     if (a.K % 32 == 0) {
+      // 256x256 tiles when they still give every CU at least one
+      const int64_t nbatch = blocks / (a.tiles_m * a.tiles_n);
+      MMArgs w = a;
+      w.tiles_m = (a.M + WD_BM - 1) / WD_BM;
+      w.tiles_n = (a.N + WD_BN - 1) / WD_BN;
+      const int64_t wblocks = w.tiles_m * w.tiles_n * nbatch;
+      if (a.M % WD_BM == 0 && a.N % WD_BN == 0 && a.K % 64 == 0 &&
+          wblocks >= device_cu_count()) {
+        mm_f32_mfma_wide_kernel<LA, LB>
+            <<<dim3(unsigned(wblocks)), WD_THREADS, 0, stream()>>>(w);
+        return;
+      }
       mm_f32_mfma_dl_kernel<LA, LB>
           <<<dim3(unsigned(blocks)), MM_THREADS, 0, stream()>>>(a);
       return;

@@ -128,3 +128,30 @@ def test_config4_full_size(gpu, M, K_, N):
         loss.backward()
         _sampled_check(host(xa.grad), G, np.ascontiguousarray(B.T), r, f"dA {a_layout}")
         _sampled_check(host(xb.grad), np.ascontiguousarray(A.T), G, r, f"dB {a_layout}")
+
+
+def _batched_T(a):
+    """Batched device operand equal to `a`, stored with its last two axes
+    swapped (a transposed view per batch)."""
+    return dev(np.ascontiguousarray(np.swapaxes(a, -1, -2))).transpose(-2, -1)
+
+
+@pytest.mark.parametrize("layout", ["NN", "TN", "NT", "TT"])
+def test_wide_tile_kernel_full_check(gpu, layout):
+    """16 x [1024, 128] @ [128, 1024]: M and N multiples of 256, K of 64,
+    and 256 tiles of 256x256 -- the wide-tile kernel's conditions -- with
+    every output compared, once written and once accumulated into C."""
+    r = rng(seed_of("wide", layout))
+    Bt, M, K_, N = 16, 1024, 128, 1024
+    a = r.standard_normal((Bt, M, K_)).astype(np.float32)
+    b = (r.standard_normal((Bt, K_, N)) / np.sqrt(K_)).astype(np.float32)
+    xa = _batched_T(a) if layout[0] == "T" else dev(a)
+    xb = _batched_T(b) if layout[1] == "T" else dev(b)
+    _check(_mm(xa, xb), a, b, f"wide {layout}")
+    old = r.standard_normal((Bt, M, N)).astype(np.float32)
+    tgt = dev(old)
+    K.matmul_into(xa, xb, tgt, accumulate=True)
+    want = O.matmul(a, b, parallel=True) + old
+    scale = O.matmul(np.abs(a).astype(np.float64), np.abs(b).astype(np.float64),
+                     parallel=True) + np.abs(old)
+    assert_rel(host(tgt), want, 1e-4, f"wide accumulate {layout}", scale=scale)
