@@ -628,7 +628,10 @@ def _summarize_mm_pmc(path: str, out_md: str) -> None:
                 "Utilisation = SQ_VALU_MFMA_BUSY_CYCLES (summed over the 1024 SIMDs) / "
                 "(1024 x kernel duration x 2.4 GHz); each v_mfma_f32_32x32x2_f32 keeps the "
                 "pipe busy 64 cycles, so this equals achieved / peak FLOP rate at 2.4 GHz. "
-                "Grid 262144 work-items = 4096x4096 outputs, 524288 = 8192x4096. "
+                "Grid in work-items: the 128x128 kernel (`mm_f32_mfma_dl_kernel`, 256 per "
+                "tile) has 65536 for a 1024x4096 output and 131072 for 8192x1024; the wide "
+                "kernel (`mm_f32_mfma_wide_kernel`, 512 per 256x256 tile) has 131072 for "
+                "4096x4096 and 262144 for 8192x4096. "
                 "Durations are from this (counter-collecting) run.\n\n")
         o.write("| kernel | grid | dispatches | avg us | MFMA instr | MFMA busy cycles | "
                 "MFMA util | LDS-wait / wave cycles | LDS bank conflicts |\n"

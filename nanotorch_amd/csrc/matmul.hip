@@ -33,6 +33,8 @@
 // When both operands are in a vector layout and K is a multiple of 32, the
 // operands skip the register round trip: mm_f32_mfma_dl_kernel stages them
 // with gfx950's direct global-to-LDS loads (same tiles, same MFMA schedule).
+// Large products (M, N multiples of 256, K of 64, a 256x256 tile per CU)
+// use mm_f32_mfma_wide_kernel: 256x256 tiles, 8 waves of 128x64.
 //
 // Other dtypes (fp64, int32, int64) use a tiled SIMT kernel that accumulates
 // in k order exactly like the reference's CPU loop (matmul.cu:33-45).
