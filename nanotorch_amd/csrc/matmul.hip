@@ -67,6 +67,12 @@ struct MMArgs {
   int64_t bsA[MM_MAX_BATCH], bsB[MM_MAX_BATCH], bsC[MM_MAX_BATCH];
   int64_t tiles_m, tiles_n;
   int accumulate;
+  // Wide kernel, split over K: blockIdx.y = s takes k in [s kslice,
+  // (s + 1) kslice) and writes its raw sum to part + s M N ([M][N]
+  // contiguous); mm_splitk_sum_kernel adds the slices.  part == nullptr: no
+  // split (kslice == K), results go to C.
+  int64_t kslice;
+  float *part;
 };
 
 // Operand tile loader: global -> registers -> LDS.  ROWS x MM_BK tile of
@@ -563,12 +569,13 @@ __global__ __launch_bounds__(WD_THREADS, 1) void mm_f32_mfma_wide_kernel(
 
   WideDirectTile<LA> ta;
   WideDirectTile<LB> tb;
-  ta.init(tc.A, tc.m0, g.sAm, g.sAk, wave, lane);
-  tb.init(tc.B, tc.n0, g.sBn, g.sBk, wave, lane);
-  // K is a multiple of 64: k-tiles come in pairs, one per stage, and the
-  // loop has a single exit (an exit between the two stages made the
+  const int64_t k0 = int64_t(blockIdx.y) * g.kslice;
+  ta.init(tc.A + k0 * g.sAk, tc.m0, g.sAm, g.sAk, wave, lane);
+  tb.init(tc.B + k0 * g.sBk, tc.n0, g.sBn, g.sBk, wave, lane);
+  // The slice is a multiple of 64: k-tiles come in pairs, one per stage,
+  // and the loop has a single exit (an exit between the two stages made the
   // compiler copy and spill the accumulators).
-  const int64_t ktiles = g.K / 32;
+  const int64_t ktiles = g.kslice / 32;
   ta.issue(sA0, 0, wave);
   tb.issue(sB0, 0, wave);
   dl_wait_and_sync();
@@ -595,11 +602,44 @@ __global__ __launch_bounds__(WD_THREADS, 1) void mm_f32_mfma_wide_kernel(
       for (int r = 0; r < 16; ++r) {
         const int64_t row =
             tc.m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-        float *dst = tc.C + row * g.sCm + col * g.sCn;
         const float v = acc[i][j][r];
-        *dst = g.accumulate ? (*dst + v) : v;
+        if (g.part) {
+          g.part[(int64_t(blockIdx.y) * g.M + row) * g.N + col] = v;
+        } else {
+          float *dst = tc.C + row * g.sCm + col * g.sCn;
+          *dst = g.accumulate ? (*dst + v) : v;
+        }
       }
     }
+}
+
+// C[m][n] (+)= part[0][m][n] + part[1][m][n] + ... in slice order (a fixed
+// order: the result does not depend on scheduling).  Four columns per
+// work-item; N is a multiple of 4.
+__global__ __launch_bounds__(256) void mm_splitk_sum_kernel(
+    const float *__restrict__ part, int S, int64_t M, int64_t N, float *C,
+    int64_t sCm, int64_t sCn, int accumulate) {
+  const int64_t n4 = N / 4;
+  const int64_t total = M * n4;
+  for (int64_t q = int64_t(blockIdx.x) * 256 + threadIdx.x; q < total;
+       q += int64_t(gridDim.x) * 256) {
+    const int64_t m = q / n4, n = (q - m * n4) * 4;
+    float4 v = *reinterpret_cast<const float4 *>(part + m * N + n);
+    for (int s = 1; s < S; ++s) {
+      const float4 w =
+          *reinterpret_cast<const float4 *>(part + (int64_t(s) * M + m) * N + n);
+      v.x = v.x + w.x;
+      v.y = v.y + w.y;
+      v.z = v.z + w.z;
+      v.w = v.w + w.w;
+    }
+    const float o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float *dst = C + m * sCm + (n + e) * sCn;
+      *dst = accumulate ? (*dst + o[e]) : o[e];
+    }
+  }
 }
 
 // ------------------------------------------------ SIMT (non-fp32) kernel
@@ -658,17 +698,40 @@ namespace {
 template <int LA, int LB> void launch_mfma(const MMArgs &a, int64_t blocks) {
   if constexpr (LA != LAY_GEN && LB != LAY_GEN) {
     if (a.K % 32 == 0) {
-      // 256x256 tiles when they still give every CU at least one
+      // 256x256 tiles when they (or, for one product, they times a split of
+      // K into 2, 4 or 8 slices of at least 1024) give every CU one
       const int64_t nbatch = blocks / (a.tiles_m * a.tiles_n);
       MMArgs w = a;
       w.tiles_m = (a.M + WD_BM - 1) / WD_BM;
       w.tiles_n = (a.N + WD_BN - 1) / WD_BN;
       const int64_t wblocks = w.tiles_m * w.tiles_n * nbatch;
-      if (a.M % WD_BM == 0 && a.N % WD_BN == 0 && a.K % 64 == 0 &&
-          wblocks >= device_cu_count()) {
-        mm_f32_mfma_wide_kernel<LA, LB>
-            <<<dim3(unsigned(wblocks)), WD_THREADS, 0, stream()>>>(w);
-        return;
+      const int64_t cus = device_cu_count();
+      if (a.M % WD_BM == 0 && a.N % WD_BN == 0 && a.K % 64 == 0) {
+        int S = 1;
+        while (wblocks * S < cus && nbatch == 1 && S < 8 &&
+               a.K % (64 * 2 * S) == 0 && a.K / (2 * S) >= 1024)
+          S *= 2;
+        if (wblocks * S >= cus) {
+          w.kslice = a.K / S;
+          if (S == 1) {
+            mm_f32_mfma_wide_kernel<LA, LB>
+                <<<dim3(unsigned(wblocks)), WD_THREADS, 0, stream()>>>(w);
+            return;
+          }
+          DeviceScratch part(size_t(S) * size_t(a.M) * size_t(a.N) *
+                             sizeof(float));
+          w.part = part.get<float>();
+          mm_f32_mfma_wide_kernel<LA, LB>
+              <<<dim3(unsigned(wblocks), unsigned(S)), WD_THREADS, 0,
+                 stream()>>>(w);
+          NT_LAUNCH_CHECK();
+          const int64_t items = a.M * (a.N / 4);
+          const unsigned grid = unsigned(
+              std::min<int64_t>((items + 255) / 256, cus * 16));
+          mm_splitk_sum_kernel<<<grid, 256, 0, stream()>>>(
+              w.part, S, a.M, a.N, a.C, a.sCm, a.sCn, a.accumulate);
+          return;
+        }
       }
       mm_f32_mfma_dl_kernel<LA, LB>
           <<<dim3(unsigned(blocks)), MM_THREADS, 0, stream()>>>(a);
@@ -783,6 +846,8 @@ int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
           batch_al = false;
       }
       g.accumulate = accumulate ? 1 : 0;
+      g.kslice = K;
+      g.part = nullptr;
       // Vector (16-byte) tile loads need the unit-stride extent and the other
       // stride to be multiples of 4 and a 16-byte aligned base.
       int la = LAY_GEN, lb = LAY_GEN;

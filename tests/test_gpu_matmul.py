@@ -155,3 +155,22 @@ def test_wide_tile_kernel_full_check(gpu, layout):
     scale = O.matmul(np.abs(a).astype(np.float64), np.abs(b).astype(np.float64),
                      parallel=True) + np.abs(old)
     assert_rel(host(tgt), want, 1e-4, f"wide accumulate {layout}", scale=scale)
+
+
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_wide_tile_split_k_full_check(gpu, accumulate):
+    """[1024, 8192] @ [8192, 2048]: 32 tiles of 256x256, so the wide kernel
+    splits K into 8 slices (one tile per CU) and sums them in slice order;
+    every output compared with an fp64 product (the bound covers fp32
+    accumulation in any order)."""
+    r = rng(seed_of("splitk", accumulate))
+    M, K_, N = 1024, 8192, 2048
+    a = r.standard_normal((M, K_)).astype(np.float32)
+    b = (r.standard_normal((K_, N)) / np.sqrt(K_)).astype(np.float32)
+    old = r.standard_normal((M, N)).astype(np.float32)
+    tgt = dev(old)
+    K.matmul_into(dev(a), dev(b), tgt, accumulate=accumulate)
+    want = a.astype(np.float64) @ b.astype(np.float64) + (old if accumulate else 0.0)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64) + (
+        np.abs(old) if accumulate else 0.0)
+    assert_rel(host(tgt), want, 1e-4, f"split-K accumulate={accumulate}", scale=scale)
