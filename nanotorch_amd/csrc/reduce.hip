@@ -43,7 +43,7 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 // columns per workgroup on wide tensors, workgroups per CU for sums and for
 // max/min.
 #ifndef NT_COL_UR
-#define NT_COL_UR 8
+#define NT_COL_UR 6 // measured: max/min axis 0 4.7 -> 5.1 TB/s against 8, sums equal
 #endif
 #ifndef NT_COL_WC
 #define NT_COL_WC 4
