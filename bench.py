@@ -447,6 +447,28 @@ def bench_next(iters: int = 12) -> dict:
     return out
 
 
+def bench_copy_reference(iters: int = 8) -> dict:
+    """The library's own contiguous copy (the elementwise engine's flat
+    kernel, nt_copy) on cold buffers: 4 pairs of 2^26 fp32 arrays (2 GB in
+    all, far beyond the 256 MB Infinity Cache) used in turn, launches back
+    to back between two events.  The practical HBM rate of a read + write
+    stream on this GPU, against which the sweep's fraction of the published
+    peak reads."""
+    n = 1 << 26
+    pairs = [(_fresh((n,)), _fresh((n,))) for _ in range(4)]
+    K.copy_view(*pairs[-1])
+    e0, e1 = _lib.Event(), _lib.Event()
+    e0.record()
+    for it in range(iters):
+        K.copy_view(*pairs[it % 4])
+    e1.record()
+    nt.sync()
+    ms = e0.elapsed_ms(e1) / iters
+    gbs = 8 * n / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": 8 * n}
+
+
 # ------------------------------------------------------------ CPU baseline
 
 
@@ -793,6 +815,9 @@ def main() -> int:
         "sweep_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
         "parts": {"elementwise_per_kernel": ew["per_kernel"]},
     }
+    copy_ref = bench_copy_reference()
+    copy_ref["sweep_vs_copy"] = round(value / copy_ref["GB/s"], 4)
+    line["parts"]["copy_reference"] = copy_ref
     if "red" in parts:
         line["parts"]["reductions"] = bench_reductions()
     if "mm" in parts:
