@@ -163,6 +163,45 @@ __global__ __launch_bounds__(256) void scatter_kernel(const T *__restrict__ src,
   }
 }
 
+// Whole rows: the view is [R, C] with unit-stride rows, one 1-D index array
+// selects along axis 0, and the iteration space is [n, C] (a row gather
+// out[i, :] = x[idx[i], :], or a row scatter x[idx[i], :] = src[i, :]).  A
+// workgroup takes row i, loads idx[i] once and moves the row in VEC-element
+// vectors; an index outside the axis is reported as in index_offsets (a
+// gather writes a zero row) and a scatter skips rows the keep mask drops.
+template <class T, int VEC, bool SCATTER>
+__global__ __launch_bounds__(256) void row_index_kernel(T *view, T *iter,
+                                                        IndexPlan p, int *err) {
+  using V = VecT<T, VEC>;
+  const int64_t n = p.shape[0], cv = p.shape[1] / VEC;
+  for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
+    if (SCATTER && p.keep && !p.keep[i * p.keep_strides[0]])
+      continue;
+    const int64_t r = p.ind[0][i * p.ind_strides[0][0]];
+    V *it_row = reinterpret_cast<V *>(iter + p.iter_offset + i * p.iter_strides[0]);
+    if (r < 0 || r >= p.view_shape[0]) {
+      if (threadIdx.x == 0)
+        *err = NT_ERR_INDEX; // the deferred-error word (host memory)
+      if constexpr (!SCATTER) {
+        V z;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j)
+          z.v[j] = T(0);
+        for (int64_t v = threadIdx.x; v < cv; v += 256)
+          it_row[v] = z;
+      }
+      continue;
+    }
+    V *vw_row = reinterpret_cast<V *>(view + p.view_offset + r * p.view_strides[0]);
+    for (int64_t v = threadIdx.x; v < cv; v += 256) {
+      if constexpr (SCATTER)
+        vw_row[v] = it_row[v];
+      else
+        it_row[v] = vw_row[v];
+    }
+  }
+}
+
 namespace {
 
 // Validates the plan's arrays and fills everything but the iteration
@@ -299,11 +338,23 @@ void run_index(const nt_view *data, const nt_view *iter, const IndexPlan &base) 
     T *dptr = static_cast<T *>(const_cast<void *>(data->data));
     T *iptr = static_cast<T *>(const_cast<void *>(iter->data));
     const int vec = index_vec<T>(data, iter, p);
+    constexpr int V = ew_vec<T>();
+    if (vec > 1 && p.out_ndim == 2 && p.view_ndim == 2 && p.nfancy == 1 &&
+        p.ind_ndim == 1 && p.is_fancy[0] && !p.is_fancy[1] &&
+        p.target[0] == 0 && p.target[1] == 1 && p.fancy_slot[0] == 0 &&
+        p.fancy_slot[1] < 0) {
+      const dim3 rgrid{unsigned(std::min<int64_t>(
+                           p.shape[0], int64_t(device_cu_count()) * 16)),
+                       1u, 1u};
+      if constexpr (V > 1)
+        row_index_kernel<T, V, SCATTER>
+            <<<rgrid, 256, 0, st>>>(dptr, iptr, p, err);
+      return;
+    }
     const int64_t groups = n / vec;
     const dim3 grid{unsigned(std::min<int64_t>((groups + 255) / 256,
                                                int64_t(device_cu_count()) * NT_IDX_WG_PER_CU)),
                     1u, 1u};
-    constexpr int V = ew_vec<T>();
 #define NT_IDX_LAUNCH(K, A, B, I32, VV)                                        \
   K<T, I32, VV><<<grid, 256, 0, st>>>(A, B, p, groups, err)
     if constexpr (SCATTER) {
