@@ -104,11 +104,20 @@ constexpr int CHUNK_BITS = CHUNK_WORDS * 64;          // 2496
 constexpr int JUMP_SPAN = CHUNK_BITS + MT_N;          // raw words per chunk
 constexpr int JUMP_RUN = 6;                           // window words per lane
 constexpr int JUMP_LANES = MT_N / JUMP_RUN;           // 52
-constexpr int JUMP_WAVES = 4;                         // substreams per group
+#ifndef NT_RNG_JUMP_WAVES
+#define NT_RNG_JUMP_WAVES 4
+#endif
+constexpr int JUMP_WAVES = NT_RNG_JUMP_WAVES;         // substreams per group
 constexpr int RAW_HALVES = 130;                       // half-blocks of raw
 constexpr int RAW_WORDS = RAW_HALVES * MT_M;          // 20280
-constexpr int GEN_BATCH = 16;    // half-blocks handed over per barrier
-constexpr int GEN_THREADS = 512; // one producer wave, seven consumer waves
+#ifndef NT_RNG_GEN_BATCH
+#define NT_RNG_GEN_BATCH 16
+#endif
+#ifndef NT_RNG_GEN_THREADS
+#define NT_RNG_GEN_THREADS 512
+#endif
+constexpr int GEN_BATCH = NT_RNG_GEN_BATCH; // half-blocks handed over per barrier
+constexpr int GEN_THREADS = NT_RNG_GEN_THREADS; // one producer wave + consumers
 static_assert(CHUNK_WORDS * JUMP_CHUNKS == POLY_WORDS, "chunking");
 static_assert((JUMP_CHUNKS - 1) * CHUNK_BITS + JUMP_SPAN <= RAW_WORDS,
               "a jump chunk reads past the raw sequence");
@@ -280,7 +289,7 @@ __global__ __launch_bounds__(64 * JUMP_WAVES) void rng_jump_kernel(
 // [w SUB_WORDS, w SUB_WORDS + count) of the round (count = min(SUB_WORDS,
 // round_words - w SUB_WORDS)) and writes their draws to out + w SUB_WORDS.
 // Wave 0 runs the recurrence in registers and hands GEN_BATCH half-blocks
-// per barrier to waves 1-7 through a double buffer in LDS; they temper,
+// per barrier to the other waves through a double buffer in LDS; they temper,
 // convert and store.  The last workgroup's producer also writes the block
 // starting at local word final_lo to final_words (the generator's new
 // state), or, when next_base is given, the window right after its range
