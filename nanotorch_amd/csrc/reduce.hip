@@ -42,6 +42,12 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 // Column-walk shape (reduce_col_kernel): rows in flight per work-item, wave
 // columns per workgroup on wide tensors, workgroups per CU for sums and for
 // max/min.
+#ifndef NT_ROW_UR
+#define NT_ROW_UR 4
+#endif
+#ifndef NT_ROW_WG_PER_CU
+#define NT_ROW_WG_PER_CU 2 // measured: full sums 6.6 -> 6.8 TB/s against 4
+#endif
 #ifndef NT_COL_UR
 #define NT_COL_UR 6 // measured: max/min axis 0 4.7 -> 5.1 TB/s against 8, sums equal
 #endif
@@ -245,8 +251,9 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
   Acc a;
   a.init();
   using V = VecT<T, VEC>;
-  // Four independent vector loads in flight per work-item, then the tail.
-  constexpr int UR = 4;
+  // NT_ROW_UR independent vector loads in flight per work-item, then the
+  // tail.
+  constexpr int UR = NT_ROW_UR;
   const int64_t step = int64_t(RED_THREADS) * VEC;
   int64_t j = j0 + int64_t(threadIdx.x) * VEC;
   for (; j + (UR - 1) * step + VEC <= j1; j += UR * step) {
@@ -574,8 +581,9 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
     for (int d = 0; d < p.keep.ndim; ++d)
       if (p.keep.strides[d] % VEC != 0)
         aligned = false;
-    // Long slices are split so that about 4 workgroups per CU stream.
-    const int64_t row_target = int64_t(device_cu_count()) * 4;
+    // Long slices are split so that about NT_ROW_WG_PER_CU workgroups per
+    // CU stream.
+    const int64_t row_target = int64_t(device_cu_count()) * NT_ROW_WG_PER_CU;
     int64_t S = 1;
     if (p.K < row_target)
       S = std::min<int64_t>(ceil_div(row_target, p.K),
