@@ -207,36 +207,86 @@ def bench_elementwise(steps: int, warmup: int) -> dict:
 # ---------------------------------------------------- config 3: reductions
 
 
-def bench_reductions(iters: int = 5) -> dict:
+def bench_reductions(iters: int = 8) -> dict:
+    """Config 3: sum / max / min forward and sum / mean / max backward over
+    axis 0, axis 1 and the full [8192, 8192] fp32 tensor, through the C ABI
+    with every output preallocated.  Each case runs `iters` launches back to
+    back between two events on the library stream (host launch overhead
+    overlaps the kernels), alternating two copies of the input and of each
+    output so that a 268 MB operand is not re-read from the 256 MB Infinity
+    Cache."""
     r = np.random.default_rng(3)
     shape = (8192, 8192)
     n = shape[0] * shape[1]
-    x = dev(r.standard_normal(shape).astype(np.float32))
-    out = {}
-    tm = Timer()
+    lib = _lib.load()
+    xs = [dev(r.standard_normal(shape).astype(np.float32)) for _ in range(2)]
+    keep: list = []
+    cases: dict[str, list] = {}
+
+    def ref(obj):
+        keep.append(obj)
+        return ctypes.byref(obj)
+
     for axes, label in (((0,), "axis0"), ((1,), "axis1"), ((0, 1), "full")):
         kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
-        g = dev(r.standard_normal(kshape if kshape else ()).astype(np.float32).reshape(kshape))
-        old = dev(r.standard_normal(shape).astype(np.float32))
-        for _ in range(iters):
-            tm.run(f"sum|{label}|fwd", lambda: K.reduce(_lib.R_SUM, x, axes, nt.float32))
-            tm.run(f"max|{label}|fwd", lambda: K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True))
-            tm.run(f"min|{label}|fwd", lambda: K.reduce(_lib.R_MIN, x, axes, nt.float32, want_aux=True))
-        _, idx, cnt = K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True)
+        k = math.prod(kshape)
+        arr = _lib.axes_array(axes)
+        keep.append(arr)
+        g = dev(r.standard_normal(k).astype(np.float32))
+        vg = K.flat_view(g._storage, (k,))
+        for op, name in ((_lib.R_SUM, "sum"), (_lib.R_MAX, "max"), (_lib.R_MIN, "min")):
+            calls = []
+            for c in range(2):
+                o = _fresh((k,))
+                aux = name != "sum"
+                idx = _fresh((k,), nt.int64) if aux else None
+                cnt = _fresh((k,), nt.int32) if aux else None
+                keep += [o, idx, cnt]
+                calls.append((lib.nt_reduce, (
+                    op, ref(view(xs[c])), arr, len(axes), ref(K.flat_view(o._storage, (k,))),
+                    ref(K.flat_view(idx._storage, (k,))) if aux else None,
+                    ref(K.flat_view(cnt._storage, (k,))) if aux else None)))
+                if name == "max" and c == 0:
+                    vi = K.flat_view(idx._storage, (k,))
+                    vc = K.flat_view(cnt._storage, (k,))
+            cases[f"{name}|{label}|fwd"] = calls
+        # the max forward's index and count, for the max backward
+        lib.nt_reduce(_lib.R_MAX, ctypes.byref(view(xs[0])), arr, len(axes),
+                      ctypes.byref(K.flat_view(_fresh((k,))._storage, (k,))),
+                      ctypes.byref(vi), ctypes.byref(vc))
+        olds = [dev(r.standard_normal(shape).astype(np.float32)) for _ in range(2)]
         gb = g.reshape(*[1 if i in axes else s for i, s in enumerate(shape)]).expand(*shape)
-        for _ in range(iters):
-            # sum backward, accumulate: old += broadcast(g)
-            tm.run(f"sum|{label}|bwd", lambda: K.inplace(_lib.ADD, old, gb))
-            tm.run(f"mean|{label}|bwd", lambda: K.reduce_bwd(_lib.R_MEAN, g, float(n // max(1, g.numel)), None, None, axes, shape, None))
-            tm.run(f"max|{label}|bwd", lambda: K.reduce_bwd(_lib.R_MAX, g, 1.0, idx, cnt, axes, shape, None))
-    nt.sync()
+        outs = [_fresh(shape) for _ in range(2)]
+        keep += [g, olds, outs, gb]
+        # sum backward, accumulate: old += broadcast(g)
+        cases[f"sum|{label}|bwd"] = [(lib.nt_inplace, (_lib.ADD, ref(view(olds[c])), ref(view(gb))))
+                                     for c in range(2)]
+        cases[f"mean|{label}|bwd"] = [(lib.nt_reduce_bwd, (
+            _lib.R_MEAN, ref(vg), float(n // k), None, None, arr, len(axes),
+            ref(view(outs[c])), 0)) for c in range(2)]
+        cases[f"max|{label}|bwd"] = [(lib.nt_reduce_bwd, (
+            _lib.R_MAX, ref(vg), 1.0, ref(vi), ref(vc), arr, len(axes),
+            ref(view(outs[c])), 0)) for c in range(2)]
     fwd_bytes = n * 4
     bwd_bytes = {"sum": 2 * n * 4, "mean": n * 4, "max": n * 4}
+    out = {}
     tot_b = tot_ms = 0.0
-    for key, ds in tm.durations().items():
-        op, label, phase = key.split("|")
-        ds = ds[1:] if len(ds) > 1 else ds  # first call allocates
-        avg = sum(ds) / len(ds)
+    order = [f"{o}|{l}|{p}" for l in ("axis0", "axis1", "full")
+             for p, ops in (("fwd", ("sum", "max", "min")), ("bwd", ("sum", "mean", "max")))
+             for o in ops]
+    for key in order:
+        calls = cases[key]
+        for fn, args in calls:  # warm-up
+            _lib.check(fn(*args))
+        e0, e1 = _lib.Event(), _lib.Event()
+        e0.record()
+        for it in range(iters):
+            fn, args = calls[it % 2]
+            _lib.check(fn(*args))
+        e1.record()
+        nt.sync()
+        avg = e0.elapsed_ms(e1) / iters
+        op, _, phase = key.split("|")
         b = fwd_bytes if phase == "fwd" else bwd_bytes[op]
         gbs = b / (avg * 1e-3) / 1e9
         out[key] = {"ms": round(avg, 5), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}

@@ -1032,8 +1032,10 @@ int nt_reduce_bwd(int32_t op, const nt_view *g, double scale, const nt_view *idx
       if (mode >= 0) {
         const FastDivU32 fd{static_cast<uint32_t>(Cdim)};
         const int64_t n4 = n / 4;
-        const int64_t blocks = std::max<int64_t>(
-            1, std::min<int64_t>(ceil_div(n4, 256), int64_t(device_cu_count()) * 16));
+        // one work-item per 16-byte group (a one-shot grid, like the
+        // elementwise engine's: a grid-stride loop over 16 workgroups per CU
+        // wrote the full-reduction gradient at 4.3 TB/s, this at 6.6)
+        const int64_t blocks = std::max<int64_t>(1, ceil_div(n4, 256));
         dispatch_float(g->dtype, [&]<class T>() {
           const T *gp = typed_ptr<const T>(g);
           const int64_t *ip = typed_ptr<const int64_t>(idx);
@@ -1052,7 +1054,7 @@ int nt_reduce_bwd(int32_t op, const nt_view *g, double scale, const nt_view *idx
           } else {
             const int64_t Cc = Cdim, Rr = n / Cdim;
             const int64_t bx = ceil_div(Cc, 256);
-            const int64_t target = int64_t(device_cu_count()) * 8;
+            const int64_t target = int64_t(device_cu_count()) * 32;
             const int64_t by = std::max<int64_t>(
                 1, std::min<int64_t>(ceil_div(target, bx), ceil_div(Rr, 16)));
             const int64_t rpb = ceil_div(Rr, by);

@@ -362,8 +362,10 @@ int nt_fill(void *data, int32_t dtype, int64_t n, double value) {
       NT_LAUNCH_CHECK();
     }
     if (n16 > 0) {
-      int64_t blocks = std::min<int64_t>((n16 + threads - 1) / threads,
-                                         int64_t(device_cu_count()) * 16);
+      // one work-item per 16 bytes: a one-shot grid writes faster than a
+      // grid-stride loop over a few workgroups per CU
+      const int64_t blocks = std::min<int64_t>((n16 + threads - 1) / threads,
+                                               (int64_t(1) << 31) - 1);
       fill_kernel_x4<<<dim3(unsigned(blocks)), threads, 0, stream()>>>(
           reinterpret_cast<uint4 *>(p + head), n16, v4);
       NT_LAUNCH_CHECK();
