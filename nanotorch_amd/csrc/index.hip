@@ -31,6 +31,11 @@ constexpr int IDX_MAX_FANCY = NT_MAX_DIMS;
 #ifndef NT_IDX_WG_PER_CU
 #define NT_IDX_WG_PER_CU 32
 #endif
+// Workgroups per CU for whole-row gathers / scatters (each takes rows in a
+// grid-stride loop).
+#ifndef NT_IDX_ROW_WG_PER_CU
+#define NT_IDX_ROW_WG_PER_CU 16
+#endif
 
 struct IndexPlan {
   int out_ndim;    // dims of the iteration space (gather: out, scatter: src)
@@ -344,7 +349,8 @@ void run_index(const nt_view *data, const nt_view *iter, const IndexPlan &base) 
         p.target[0] == 0 && p.target[1] == 1 && p.fancy_slot[0] == 0 &&
         p.fancy_slot[1] < 0) {
       const dim3 rgrid{unsigned(std::min<int64_t>(
-                           p.shape[0], int64_t(device_cu_count()) * 16)),
+                           p.shape[0], int64_t(device_cu_count()) *
+                                           NT_IDX_ROW_WG_PER_CU)),
                        1u, 1u};
       if constexpr (V > 1)
         row_index_kernel<T, V, SCATTER>

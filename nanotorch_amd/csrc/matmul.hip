@@ -46,6 +46,11 @@ namespace nt {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// Largest split of K for a single product with fewer wide tiles than CUs.
+#ifndef NT_MM_SPLITK_MAX
+#define NT_MM_SPLITK_MAX 8
+#endif
+
 constexpr int MM_BM = 128, MM_BN = 128, MM_BK = 32, MM_THREADS = 256;
 constexpr int MM_KPAD = MM_BK + 4;  // [mn][k] row length (floats)
 constexpr int MM_MNPAD = MM_BM + 4; // [k][mn] row length (floats)
@@ -708,7 +713,7 @@ template <int LA, int LB> void launch_mfma(const MMArgs &a, int64_t blocks) {
       const int64_t cus = device_cu_count();
       if (a.M % WD_BM == 0 && a.N % WD_BN == 0 && a.K % 64 == 0) {
         int S = 1;
-        while (wblocks * S < cus && nbatch == 1 && S < 8 &&
+        while (wblocks * S < cus && nbatch == 1 && S < NT_MM_SPLITK_MAX &&
                a.K % (64 * 2 * S) == 0 && a.K / (2 * S) >= 1024)
           S *= 2;
         if (wblocks * S >= cus) {
