@@ -51,6 +51,16 @@ namespace nt {
 constexpr int EW_THREADS = 256;
 constexpr int EW_TILE = 64;
 constexpr int EW_TILE_PAD = 65;
+// LDS tile buffers in the transposing kernel.  Two let consecutive exchange
+// rounds skip the barrier between them; one halves the kernel's LDS (16.6 KB
+// for fp32), which doubles the workgroups a CU can hold.  Measured on the
+// [4096, 4096] sweep, three alternating pairs on one MI355X: one buffer
+// 5599-5628 GB/s against 5568-5594 GB/s with two.
+#ifndef NT_TILE_LDS_BUFS
+#define NT_TILE_LDS_BUFS 1
+#endif
+constexpr int EW_TILE_BUFS = NT_TILE_LDS_BUFS;
+static_assert(EW_TILE_BUFS == 1 || EW_TILE_BUFS == 2, "one or two tile buffers");
 
 template <class T, int N> struct PtrPack {
   T *p[N > 0 ? N : 1];
@@ -284,7 +294,7 @@ __global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
     F f) {
   constexpr int T = EW_TILE, P = EW_TILE_PAD, EL = 4;
   constexpr size_t LB = sizeof(TI) > sizeof(TO) ? sizeof(TI) : sizeof(TO);
-  __shared__ __align__(16) unsigned char lds_raw[2][T * P * LB];
+  __shared__ __align__(16) unsigned char lds_raw[EW_TILE_BUFS][T * P * LB];
   const int t = threadIdx.x;
   // Tile order: groups of 8 tile-rows walked column by column (measured on
   // the [4096, 4096] sweep: 2% faster overall than row-major tile order,
@@ -344,15 +354,20 @@ __global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
       }
     }
   }
-  // LDS exchange of COL inputs: one round (and one barrier) per operand,
-  // alternating between the two buffers.  A buffer is rewritten two rounds
-  // after it was read, and every work-item has passed the barrier of the
-  // round in between, so its reads are complete.
+  // LDS exchange of COL inputs: one round (and one barrier) per operand.
+  // With two buffers the rounds alternate between them: a buffer is
+  // rewritten two rounds after it was read, and every work-item has passed
+  // the barrier of the round in between, so its reads are complete.  With
+  // one buffer each round after the first waits at a barrier of its own
+  // before it writes.  The number of rounds follows the layout masks, which
+  // are kernel arguments, so every such barrier is workgroup-uniform.
   int rnd = 0;
 #pragma unroll
   for (int k = 0; k < NI; ++k) {
     if (col_in & (1u << k)) {
-      TI *lds = reinterpret_cast<TI *>(lds_raw[rnd & 1]);
+      if (EW_TILE_BUFS == 1 && rnd > 0)
+        __syncthreads();
+      TI *lds = reinterpret_cast<TI *>(lds_raw[rnd % EW_TILE_BUFS]);
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
         const int f_ = t + EW_THREADS * i;
@@ -393,7 +408,9 @@ __global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
     TO *p = out.p[m];
     const int64_t sr = sout.r[m], sc = sout.c[m];
     if (col_out & (1u << m)) {
-      TO *lds = reinterpret_cast<TO *>(lds_raw[rnd & 1]);
+      if (EW_TILE_BUFS == 1 && rnd > 0)
+        __syncthreads();
+      TO *lds = reinterpret_cast<TO *>(lds_raw[rnd % EW_TILE_BUFS]);
       ++rnd;
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
