@@ -740,16 +740,22 @@ def summarize(kind: str, dirs: list[str]) -> None:
         raise SystemExit(f"unknown profile kind {kind}")
 
     def load(path, counter):
+        # per-kernel average, plus the copy kernel's readings by grid size:
+        # the same copy kernel also runs at 2^26 elements (the cold-copy
+        # reference), and only the 2^24 --calib copies calibrate
         d: dict[str, list[float]] = {}
+        copies: dict[int, list[float]] = {}
         for r in csv.DictReader(open(os.path.join(path, "run_counter_collection.csv"))):
             if r.get("Counter_Name") == counter:
                 d.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
-        return {k: sum(v) / len(v) for k, v in d.items()}
+                if "CastOp<float, float>" in r["Kernel_Name"]:
+                    copies.setdefault(int(r["Grid_Size"]), []).append(float(r["Counter_Value"]))
+        calib = copies[min(copies)]  # the smallest copies: 2^24 fp32
+        return {k: sum(v) / len(v) for k, v in d.items()}, sum(calib) / len(calib)
 
-    fch, wr = load(dirs[0], "FETCH_SIZE"), load(dirs[1], "WRITE_SIZE")
-    copy = [k for k in fch if "CastOp<float, float>" in k][0]  # the --calib copies
-    fs = 64 * 1024 / fch[copy]  # counters are KiB; the copy reads 64 MiB
-    ws = 64 * 1024 / wr[copy]  # and writes 64 MiB
+    (fch, fcopy), (wr, wcopy) = load(dirs[0], "FETCH_SIZE"), load(dirs[1], "WRITE_SIZE")
+    fs = 64 * 1024 / fcopy  # counters are KiB; the copy reads 64 MiB
+    ws = 64 * 1024 / wcopy  # and writes 64 MiB
     per, rows = {}, []
     for k in fch:
         kk = _sweep_key(k)
@@ -770,7 +776,7 @@ def summarize(kind: str, dirs: list[str]) -> None:
         o.write("Summarised with `python bench.py --summarize traffic gpurun_out/prof_fetch "
                 "gpurun_out/prof_write` (also writes traffic.json, read by the roofline).\n\n")
         o.write(f"Calibration: a plain copy of 2^24 fp32 (64 MiB read, 64 MiB written) reads "
-                f"FETCH_SIZE {fch[copy] / 1024:.1f} MiB and WRITE_SIZE {wr[copy] / 1024:.1f} MiB per "
+                f"FETCH_SIZE {fcopy / 1024:.1f} MiB and WRITE_SIZE {wcopy / 1024:.1f} MiB per "
                 f"dispatch, so FETCH_SIZE is scaled by {fs:.3f} and WRITE_SIZE by {ws:.3f}.\n\n")
         o.write("| kernel | FETCH_SIZE MiB | WRITE_SIZE MiB | scaled traffic MiB | algorithmic MiB |\n"
                 "|---|---|---|---|---|\n")
