@@ -58,7 +58,7 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 #define NT_COL_WG_SUM 1
 #endif
 #ifndef NT_COL_WG_SEL
-#define NT_COL_WG_SEL 2
+#define NT_COL_WG_SEL 2 // measured: max/min axis 0 4.3 / 5.0 / 4.6 / 4.0 TB/s at 1 / 2 / 4 / 8
 #endif
 
 // ------------------------------------------------------------ accumulators
