@@ -39,7 +39,7 @@
 // Vector groups per thread, and threads per workgroup, in the contiguous
 // (flat) kernel.
 #ifndef NT_FLAT_UNROLL
-#define NT_FLAT_UNROLL 2
+#define NT_FLAT_UNROLL 1 // measured, whole sweep on one box: 5659 GB/s mean against 5634 (2), 5535 (4)
 #endif
 #ifndef NT_FLAT_THREADS
 #define NT_FLAT_THREADS 512 // measured: sweep +0.5% against 256 and 128
