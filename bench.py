@@ -337,22 +337,64 @@ def bench_matmul(iters: int = 5) -> dict:
 # ---------------------------------------------------------- config 5: MLP
 
 
-def bench_mlp(steps: int = 20) -> dict:
-    r = np.random.default_rng(5)
-    B, D_in = 8192, 1024
-    dims = [1024, 4096, 4096, 4096, 1000]
-    X = dev(r.standard_normal((B, D_in)).astype(np.float32))
-    T = dev(r.standard_normal((B, 1000)).astype(np.float32))
-    layers = []
+C5_DIMS = [1024, 4096, 4096, 4096, 1000]
+C5_ACTS = ["tanh", "sigmoid", "relu"]
+C5_BATCH = 8192
+C5_LR = 1e-3
+C5_TRACE = os.path.join(ROOT, "tests", "golden", "config5_trace.npz")
+
+
+def config5_inputs(seed: int = 5):
+    """Config 5's synthetic inputs, drawn in this order from
+    numpy.random.default_rng(seed): X [8192, 1024] ~ N(0,1), T [8192, 1000]
+    ~ N(0,1), then W_i [fan_in, fan_out] ~ N(0, 2/fan_in) (He-normal) for the
+    four layers; biases are zero (nn.Linear's init, as the reference's
+    Linear(bias=True)).  Returns float32 arrays (x, t, [(W, b), ...])."""
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((C5_BATCH, C5_DIMS[0])).astype(np.float32)
+    t = r.standard_normal((C5_BATCH, C5_DIMS[-1])).astype(np.float32)
+    params = []
     for i in range(4):
-        lin = nn.Linear(dims[i], dims[i + 1])
-        w = (r.standard_normal((dims[i], dims[i + 1])) * np.sqrt(2.0 / dims[i])).astype(np.float32)
+        w = (r.standard_normal((C5_DIMS[i], C5_DIMS[i + 1])) * np.sqrt(2.0 / C5_DIMS[i])).astype(np.float32)
+        params.append((w, np.zeros(C5_DIMS[i + 1], dtype=np.float32)))
+    return x, t, params
+
+
+def config5_model(params):
+    """Sequential(Linear, Tanh, Linear, Sigmoid, Linear, ReLU, Linear) on the
+    device with the given (W, b) arrays, and its Linear layers."""
+    layers = []
+    for w, b in params:
+        lin = nn.Linear(w.shape[0], w.shape[1])
         lin._W = dev(w)
         lin._W.enable_grad()
+        lin._b = dev(b)
+        lin._b.enable_grad()
         layers.append(lin)
     model = nn.Sequential(layers[0], nn.Tanh(), layers[1], nn.Sigmoid(), layers[2],
-                             nn.ReLU(), layers[3])
-    opt = nn.GradientDescent(model.parameters(), lr=1e-3)
+                          nn.ReLU(), layers[3])
+    return model, layers
+
+
+def config5_reference_trace():
+    """The CPU reference's 20-step loss trace for config5_inputs(5) (the
+    committed fixture, written by tests/golden/make_config5_trace.py), as
+    (losses, losses_exact64): the reference's literal losses, whose MeanOp
+    sums 8,192,000 squared errors left to right in fp32 (~1.1% low here),
+    and the mean of the same squared errors summed in fp64.  None when the
+    fixture is absent."""
+    if not os.path.exists(C5_TRACE):
+        return None
+    with np.load(C5_TRACE, allow_pickle=False) as z:
+        return [float(v) for v in z["losses"]], [float(v) for v in z["losses_exact64"]]
+
+
+def bench_mlp(steps: int = 20) -> dict:
+    x, t, params = config5_inputs(5)
+    X, T = dev(x), dev(t)
+    model, _ = config5_model(params)
+    del x, t, params
+    opt = nn.GradientDescent(model.parameters(), lr=C5_LR)
     losses = []
     times = []
     for s in range(steps):
@@ -372,9 +414,25 @@ def bench_mlp(steps: int = 20) -> dict:
     steady = ms[2:] if len(ms) > 3 else ms
     avg = sum(steady) / len(steady)
     flop = 1_988_032_987_136  # per step; layer-1 dX is not computed (X needs no grad)
-    return {"step/s": round(1000.0 / avg, 3), "ms_per_step": round(avg, 3),
-            "matmul_TFLOP/s": round(flop / (avg * 1e-3) / 1e12, 2),
-            "loss_trace": [round(v, 7) for v in trace], "steps": steps}
+    out = {"step/s": round(1000.0 / avg, 3), "ms_per_step": round(avg, 3),
+           "matmul_TFLOP/s": round(flop / (avg * 1e-3) / 1e12, 2),
+           "loss_trace": [round(v, 7) for v in trace], "steps": steps}
+    ref = config5_reference_trace()
+    if ref is not None:
+        # per-step relative deviation from the CPU reference's run of the
+        # same 20 steps on the same seeded inputs: against the mean of its
+        # squared errors (bar: 1e-4), and against its literal loss, which
+        # carries its sequential fp32 summation error
+        lit, exact = ref
+        k = min(len(lit), len(trace))
+        out["loss_max_rel_dev_vs_cpu_ref_exact_sum"] = float(
+            max(abs(a - b) / abs(b) for a, b in zip(trace[:k], exact[:k])))
+        out["loss_max_rel_dev_vs_cpu_ref_literal"] = float(
+            max(abs(a - b) / abs(b) for a, b in zip(trace[:k], lit[:k])))
+        out["cpu_ref_literal_vs_exact_sum"] = float(
+            max(abs(a - b) / abs(b) for a, b in zip(lit[:k], exact[:k])))
+        out["loss_steps_compared"] = k
+    return out
 
 
 # --------------------------------------------- next rows beside the path

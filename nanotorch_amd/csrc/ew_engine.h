@@ -669,20 +669,39 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
     for (int m = 0; m < NO; ++m)
       if (reinterpret_cast<uintptr_t>(pout.p[m]) % (sizeof(TO) * VBIG) != 0)
         aligned = false;
-    const int64_t nvec = aligned ? n / VBIG : n;
-    const int64_t blocks = std::max<int64_t>(
-        1, (nvec + FLAT_THREADS * UNROLL - 1) / (FLAT_THREADS * UNROLL));
-    const dim3 grid{unsigned(blocks), 1u, 1u};
-    if (aligned && ntl)
-      ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, true, F>
-          <<<grid, FLAT_THREADS, 0, s>>>(pin, smask, pout, nvec, n, f);
-    else if (aligned)
-      ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, false, F>
-          <<<grid, FLAT_THREADS, 0, s>>>(pin, smask, pout, nvec, n, f);
-    else
-      ew_flat_kernel<TI, TO, NI, NO, 1, UNROLL, false, F>
-          <<<grid, FLAT_THREADS, 0, s>>>(pin, smask, pout, n, n, f);
-    NT_LAUNCH_CHECK();
+    const int VEC = aligned ? VBIG : 1;
+    const int64_t nvec = n / VEC;
+    // One work-item per UNROLL vector groups in a one-shot grid; a dispatch
+    // holds fewer than 2^32 work-items, so a longer range (e.g. an
+    // unaligned view past 2^32 elements) goes out in chunks of 2^30 groups,
+    // the trailing partial group with the last chunk.
+    constexpr int64_t CHUNK = int64_t(1) << 30;
+    int64_t v0 = 0;
+    do {
+      const int64_t cv = std::min(CHUNK, nvec - v0);
+      const int64_t cn = (v0 + cv == nvec) ? n - v0 * VEC : cv * VEC;
+      PtrPack<const TI, NI> cin = pin;
+      PtrPack<TO, NO> cout = pout;
+      for (int k = 0; k < NI; ++k)
+        if (!(smask & (1u << k)))
+          cin.p[k] += v0 * VEC;
+      for (int m = 0; m < NO; ++m)
+        cout.p[m] += v0 * VEC;
+      const int64_t blocks = std::max<int64_t>(
+          1, (cv + FLAT_THREADS * UNROLL - 1) / (FLAT_THREADS * UNROLL));
+      const dim3 grid{unsigned(blocks), 1u, 1u};
+      if (aligned && ntl)
+        ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, true, F>
+            <<<grid, FLAT_THREADS, 0, s>>>(cin, smask, cout, cv, cn, f);
+      else if (aligned)
+        ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, false, F>
+            <<<grid, FLAT_THREADS, 0, s>>>(cin, smask, cout, cv, cn, f);
+      else
+        ew_flat_kernel<TI, TO, NI, NO, 1, UNROLL, false, F>
+            <<<grid, FLAT_THREADS, 0, s>>>(cin, smask, cout, cv, cn, f);
+      NT_LAUNCH_CHECK();
+      v0 += cv;
+    } while (v0 < nvec);
     return;
   }
 
@@ -792,7 +811,7 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
     const int64_t tiles_r = (R + EW_TILE - 1) / EW_TILE;
     const int64_t tiles_c = (C + EW_TILE - 1) / EW_TILE;
     const int64_t blocks = tiles_r * tiles_c;
-    if (blocks < (int64_t(1) << 31)) {
+    if (blocks * EW_THREADS < (int64_t(1) << 32)) {
       const dim3 grid{unsigned(blocks), 1u, 1u};
       if (vec4 && ntl)
         ew_tile4_kernel<TI, TO, NI, NO, true, F><<<grid, EW_THREADS, 0, s>>>(

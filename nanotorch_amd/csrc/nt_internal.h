@@ -7,6 +7,7 @@
 #include <array>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -73,9 +74,17 @@ private:
 // Checks the launch that was just queued.
 #define NT_LAUNCH_CHECK() NT_HIP_CHECK(hipGetLastError())
 
+// One lock for the library's process-wide state (initialisation, the
+// stream, the generator, cached work buffers): every entry point holds it for
+// its whole body, so calls from several host threads run one at a time, as
+// the reference's binding serialises them under the GIL.  The allocator has
+// its own lock as well (caching_allocator.h).
+std::recursive_mutex &api_mutex();
+
 // Runs f, converting exceptions into a status code plus a thread-local
 // message.  Every extern "C" entry point is a guard() around its body.
 template <class F> int guard(F &&f) {
+  std::lock_guard<std::recursive_mutex> lock(api_mutex());
   try {
     ensure_init();
     f();

@@ -9,6 +9,7 @@
 #include <map>
 #include <mutex>
 
+#include "caching_allocator.h"
 #include "ew_engine.h"
 
 namespace nt {
@@ -34,84 +35,29 @@ Runtime &rt() {
 }
 
 // ---------------------------------------------------------------- allocator
-//
-// Stream-ordered caching allocator.  Every kernel and copy of the library runs
-// on one stream, so a block freed by the host can be handed to the next
-// request immediately: any later use is queued after the last use of the
-// previous owner.  Requests are rounded up to 512 B (small) or 2 MiB (large)
-// so that the free lists see a handful of distinct sizes per workload.  On
-// an out-of-memory error the cache is returned to HIP and the request
-// retried once.  The reference's allocator buckets by 256 B and never frees
-// (src/cpp/allocator.cpp:16-36).
-struct CachingAllocator {
-  std::multimap<size_t, void *> free_blocks; // size -> ptr
-  std::map<void *, size_t> live;             // ptr -> size
-  size_t bytes_in_use = 0;
-  size_t bytes_cached = 0;
 
-  static size_t round_size(size_t n) {
-    if (n == 0)
-      n = 1;
-    const size_t small = 512, large = size_t(2) << 20;
-    if (n < large)
-      return (n + small - 1) / small * small;
-    return (n + large - 1) / large * large;
-  }
-
-  void *alloc(size_t nbytes) {
-    size_t sz = round_size(nbytes);
-    // Best fit among cached blocks no more than 25% larger than asked.
-    auto it = free_blocks.lower_bound(sz);
-    if (it != free_blocks.end() && it->first <= sz + sz / 4) {
-      void *p = it->second;
-      size_t bsz = it->first;
-      free_blocks.erase(it);
-      bytes_cached -= bsz;
-      live[p] = bsz;
-      bytes_in_use += bsz;
-      return p;
-    }
+struct HipBackend {
+  static void *raw_alloc(size_t n, bool *oom) {
     void *p = nullptr;
-    hipError_t e = hipMalloc(&p, sz);
-    if (e == hipErrorOutOfMemory) {
-      (void)hipGetLastError();
-      release_cache();
-      e = hipMalloc(&p, sz);
-    }
-    if (e != hipSuccess) {
-      (void)hipGetLastError();
-      fail(NT_ERR_OOM, "device allocation of " + std::to_string(sz) +
-                           " bytes failed: " + hipGetErrorString(e));
-    }
-    live[p] = sz;
-    bytes_in_use += sz;
-    return p;
+    const hipError_t e = hipMalloc(&p, n);
+    if (e == hipSuccess)
+      return p;
+    (void)hipGetLastError();
+    *oom = (e == hipErrorOutOfMemory);
+    return nullptr;
   }
-
-  void free(void *p) {
-    auto it = live.find(p);
-    if (it == live.end())
-      fail(NT_ERR_RUNTIME, "nt_free: pointer not allocated by nt_malloc");
-    free_blocks.emplace(it->second, p);
-    bytes_cached += it->second;
-    bytes_in_use -= it->second;
-    live.erase(it);
+  static void raw_free(void *p) { NT_HIP_CHECK(hipFree(p)); }
+  static void sync() { NT_HIP_CHECK(hipStreamSynchronize(rt().stream)); }
+  [[noreturn]] static void fail_oom(const std::string &msg) {
+    fail(NT_ERR_OOM, msg);
   }
-
-  void release_cache() {
-    if (free_blocks.empty())
-      return;
-    // Blocks may still be read by queued work of their previous owner.
-    NT_HIP_CHECK(hipStreamSynchronize(rt().stream));
-    for (auto &kv : free_blocks)
-      NT_HIP_CHECK(hipFree(kv.second));
-    free_blocks.clear();
-    bytes_cached = 0;
+  [[noreturn]] static void fail_bad_free(const std::string &msg) {
+    fail(NT_ERR_RUNTIME, msg);
   }
 };
 
-CachingAllocator &allocator() {
-  static CachingAllocator a;
+CachingAllocator<HipBackend> &allocator() {
+  static CachingAllocator<HipBackend> a;
   return a;
 }
 
@@ -141,6 +87,11 @@ __global__ void fill_kernel_x4(uint4 *p, int64_t n16, uint4 v) {
 } // namespace
 
 void set_last_error(const std::string &msg) { g_last_error = msg; }
+
+std::recursive_mutex &api_mutex() {
+  static std::recursive_mutex m;
+  return m;
+}
 
 void ensure_init() {
   Runtime &r = rt();
@@ -283,12 +234,7 @@ int nt_empty_cache(void) {
 }
 
 int nt_memory_stats(size_t *bytes_in_use, size_t *bytes_cached) {
-  return guard([&] {
-    if (bytes_in_use)
-      *bytes_in_use = allocator().bytes_in_use;
-    if (bytes_cached)
-      *bytes_cached = allocator().bytes_cached;
-  });
+  return guard([&] { allocator().stats(bytes_in_use, bytes_cached); });
 }
 
 int nt_memcpy_h2d(void *dst, const void *src, size_t nbytes) {
@@ -363,9 +309,11 @@ int nt_fill(void *data, int32_t dtype, int64_t n, double value) {
     }
     if (n16 > 0) {
       // one work-item per 16 bytes: a one-shot grid writes faster than a
-      // grid-stride loop over a few workgroups per CU
+      // grid-stride loop over a few workgroups per CU; past 2^30 work-items
+      // (16 GiB) the kernel's grid-stride loop takes the rest, since a
+      // dispatch holds fewer than 2^32 work-items
       const int64_t blocks = std::min<int64_t>((n16 + threads - 1) / threads,
-                                               (int64_t(1) << 31) - 1);
+                                               (int64_t(1) << 30) / threads);
       fill_kernel_x4<<<dim3(unsigned(blocks)), threads, 0, stream()>>>(
           reinterpret_cast<uint4 *>(p + head), n16, v4);
       NT_LAUNCH_CHECK();

@@ -22,8 +22,13 @@
 // IEEE rounding as in the reference, and the std:: math calls resolve to the
 // host libm exactly as the reference's CPU path does.
 //
-// or_matmul_omp computes each output with the same sequential k loop, only
-// spreading outputs over OpenMP threads: bit-identical to or_matmul.
+// or_matmul_omp computes each output with the same sequential k loop as
+// or_matmul -- acc = 0, then acc = acc + a_k * b_k for k = 0, 1, ..., K-1,
+// one rounding per * and per + -- but in a cache-blocked i-k-j order spread
+// over OpenMP threads: the k order of every output is unchanged, so the result
+// is bit-identical to or_matmul (vector width changes nothing either: each
+// lane is one output).
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -37,6 +42,7 @@
 #ifdef _OPENMP
 #include <omp.h>
 #endif
+#include <immintrin.h>
 
 extern "C" {
 typedef struct or_view {
@@ -210,6 +216,89 @@ template <class O> MatItem<O> neutral(int op) {
                       std::numeric_limits<O>::lowest()};
   return MatItem<O>{std::numeric_limits<int64_t>::max(),
                     std::numeric_limits<O>::max()};
+}
+
+} // namespace
+
+// ----------------------------------------------------- blocked product
+// C[M,N] = A[M,K] . B[K,N] on packed row-major operands.  C is zeroed first,
+// then every C[i][j] receives C[i][j] + A[i][k] * B[k][j] for k = 0, 1, ...
+// in increasing order (k blocks in order, k increasing inside a block): the
+// per-output operation sequence of the reference's loop (matmul.cu:33-45).
+namespace {
+
+constexpr int64_t MB_I = 64, MB_J = 256, MB_K = 256;
+
+// 4 x 64 register tile of C over k in [k0, k1): AVX-512, separate multiply
+// and add (no FMA), one output per lane.
+__attribute__((target("avx512f"))) void mm_tile4x64_avx512(
+    const float *A, const float *B, float *C, int64_t K, int64_t N, int64_t i,
+    int64_t j, int64_t k0, int64_t k1) {
+  __m512 c[4][4];
+  for (int r = 0; r < 4; ++r)
+    for (int v = 0; v < 4; ++v)
+      c[r][v] = _mm512_loadu_ps(C + (i + r) * N + j + 16 * v);
+  for (int64_t k = k0; k < k1; ++k) {
+    const float *b = B + k * N + j;
+    __m512 b0 = _mm512_loadu_ps(b), b1 = _mm512_loadu_ps(b + 16),
+           b2 = _mm512_loadu_ps(b + 32), b3 = _mm512_loadu_ps(b + 48);
+    for (int r = 0; r < 4; ++r) {
+      __m512 a = _mm512_set1_ps(A[(i + r) * K + k]);
+      c[r][0] = _mm512_add_ps(c[r][0], _mm512_mul_ps(a, b0));
+      c[r][1] = _mm512_add_ps(c[r][1], _mm512_mul_ps(a, b1));
+      c[r][2] = _mm512_add_ps(c[r][2], _mm512_mul_ps(a, b2));
+      c[r][3] = _mm512_add_ps(c[r][3], _mm512_mul_ps(a, b3));
+    }
+  }
+  for (int r = 0; r < 4; ++r)
+    for (int v = 0; v < 4; ++v)
+      _mm512_storeu_ps(C + (i + r) * N + j + 16 * v, c[r][v]);
+}
+
+template <class T>
+void mm_block_scalar(const T *A, const T *B, T *C, int64_t K, int64_t N,
+                     int64_t i0, int64_t i1, int64_t j0, int64_t j1, int64_t k0,
+                     int64_t k1) {
+  for (int64_t i = i0; i < i1; ++i)
+    for (int64_t k = k0; k < k1; ++k) {
+      const T a = A[i * K + k];
+      const T *b = B + k * N;
+      T *c = C + i * N;
+      for (int64_t j = j0; j < j1; ++j)
+        c[j] += a * b[j];
+    }
+}
+
+template <class T>
+void mm_blocked(const T *A, const T *B, T *C, int64_t M, int64_t K,
+                int64_t N) {
+  for (int64_t x = 0; x < M * N; ++x)
+    C[x] = static_cast<T>(0.0);
+  bool wide = false;
+  if constexpr (std::is_same_v<T, float>)
+    wide = __builtin_cpu_supports("avx512f");
+  const int64_t nbi = (M + MB_I - 1) / MB_I, nbj = (N + MB_J - 1) / MB_J;
+#pragma omp parallel for schedule(dynamic)
+  for (int64_t t = 0; t < nbi * nbj; ++t) {
+    const int64_t i0 = (t / nbj) * MB_I, j0 = (t % nbj) * MB_J;
+    const int64_t i1 = std::min(M, i0 + MB_I), j1 = std::min(N, j0 + MB_J);
+    for (int64_t k0 = 0; k0 < K; k0 += MB_K) {
+      const int64_t k1 = std::min(K, k0 + MB_K);
+      int64_t iv = i0, jv = j0;
+      if constexpr (std::is_same_v<T, float>) {
+        if (wide) {
+          iv = i0 + (i1 - i0) / 4 * 4;
+          jv = j0 + (j1 - j0) / 64 * 64;
+          for (int64_t i = i0; i < iv; i += 4)
+            for (int64_t j = j0; j < jv; j += 64)
+              mm_tile4x64_avx512(A, B, C, K, N, i, j, k0, k1);
+        }
+      }
+      // the rest of the block: columns right of the vector tiles, rows below
+      mm_block_scalar(A, B, C, K, N, i0, iv, jv, j1, k0, k1);
+      mm_block_scalar(A, B, C, K, N, iv, i1, j0, j1, k0, k1);
+    }
+  }
 }
 
 } // namespace
@@ -396,7 +485,34 @@ static int matmul_impl(const or_view *a, const or_view *b, void *out,
       const T *A = static_cast<const T *>(a->data);
       const T *B = static_cast<const T *>(b->data);
       T *C = static_cast<T *>(out);
-      auto one = [&](int64_t idx) {
+      if (parallel) {
+        // Per batch index: pack both operands row-major (a copy, exact),
+        // then the blocked product.
+        const int64_t nbatch = (M * N) ? total / (M * N) : 0;
+        std::vector<T> pa(size_t(M * K)), pb(size_t(K * N));
+        for (int64_t bi = 0; bi < nbatch; ++bi) {
+          int64_t oa = a->offset, ob = b->offset, r = bi;
+          for (int d = nd - 3; d >= 0; --d) {
+            const int64_t l = r % oshape[d];
+            r /= oshape[d];
+            oa += l * a->strides[d];
+            ob += l * b->strides[d];
+          }
+#pragma omp parallel for schedule(static)
+          for (int64_t i = 0; i < M; ++i)
+            for (int64_t c = 0; c < K; ++c)
+              pa[size_t(i * K + c)] =
+                  A[oa + i * a->strides[nd - 2] + c * a->strides[nd - 1]];
+#pragma omp parallel for schedule(static)
+          for (int64_t c = 0; c < K; ++c)
+            for (int64_t j = 0; j < N; ++j)
+              pb[size_t(c * N + j)] =
+                  B[ob + c * b->strides[nd - 2] + j * b->strides[nd - 1]];
+          mm_blocked(pa.data(), pb.data(), C + bi * M * N, M, K, N);
+        }
+        return;
+      }
+      for (int64_t idx = 0; idx < total; ++idx) {
         // loc = row-major coordinates of output idx (matmul.cu:31-56)
         int64_t loc[8];
         int64_t r = idx;
@@ -417,14 +533,6 @@ static int matmul_impl(const or_view *a, const or_view *b, void *out,
           acc += A[i1] * B[i2];
         }
         C[idx] = acc;
-      };
-      if (parallel) {
-#pragma omp parallel for schedule(static)
-        for (int64_t idx = 0; idx < total; ++idx)
-          one(idx);
-      } else {
-        for (int64_t idx = 0; idx < total; ++idx)
-          one(idx);
       }
     });
   });

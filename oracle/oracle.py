@@ -323,13 +323,18 @@ def mean_fwd(x: np.ndarray, axes) -> np.ndarray:
 # ------------------------------------------------------------ MLP step
 
 
-def mlp_step(params, x, t, acts, lr: float, parallel: bool = True):
+def mlp_step(params, x, t, acts, lr: float, parallel: bool = True, stats: dict | None = None):
     """One training step of Sequential(Linear, act, ..., Linear) with loss
     mean((Y - T)**2) and GradientDescent, restating nn/module.py:64-76,
     train_mlp_basic.py:45-55, optimizers.py:45-51 and the backward chains of
     each op.  params: list of (W, b) float32 arrays, updated in place.
     acts: activation names between layers ('relu', 'tanh', 'sigmoid').
-    Returns the loss (a numpy float32 scalar) before the update."""
+    Returns the loss (a numpy float32 scalar) before the update.
+
+    With `stats` (a dict), also stores stats["sq_sum64"], the float64 sum of
+    the squared-error tensor (Y - T)**2 the loss is the mean of, and
+    stats["numel"]: the loss with the reference's sequential fp32
+    summation error taken out (the backward does not depend on it)."""
     mm = lambda a, b: matmul(a, b, parallel=parallel)  # noqa: E731
     hs = [x]  # layer inputs
     zs_saved = []  # saved activation outputs
@@ -354,6 +359,9 @@ def mlp_step(params, x, t, acts, lr: float, parallel: bool = True):
     d = binary(SUB, Y, t)
     sq = pow_scalar(d, 2)
     loss = mean_fwd(sq, tuple(range(sq.ndim)))
+    if stats is not None:
+        stats["sq_sum64"] = float(sq.astype(np.float64).sum())
+        stats["numel"] = int(sq.size)
     # backward: loss grad 1.0 -> MeanOp: expand(g) / denom
     g0 = np.array(1.0, dtype=np.float32)
     gs = binary(DIV, bcast(g0, sq.shape), bcast(scalar(sq.size, np.float32), sq.shape))

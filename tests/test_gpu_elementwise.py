@@ -313,24 +313,66 @@ def test_binary_backward_kernel(gpu, name, op, oop, need, acc):
 # ------------------------------------------------------------ config 2 size
 
 
+C2_UNARY = {n: (op, oop, chain, dom, saved) for n, op, oop, chain, dom, saved in UNARY_BWD}
+C2_OPS = ["add", "sub", "mul", "div", "neg", "exp", "log", "sqrt", "pow", "relu", "sigmoid", "tanh"]
+
+
 @pytest.mark.parametrize("layout", ["contig", "transposed"])
-def test_config2_full_size(gpu, layout):
-    """[4096, 4096] (2^24 elements): mul forward and fused backward
-    (accumulate), tanh forward, both layouts, against the oracle."""
-    r = rng(11)
+@pytest.mark.parametrize("name", C2_OPS)
+def test_config2_full_size(gpu, name, layout):
+    """Config 2 at its size, [4096, 4096] (2^24 elements), laid out as the
+    sweep runs it: every tensor input contiguous, or every tensor input a
+    `.T` view (the accumulation targets too); upstream g contiguous.  Forward,
+    then the fused backward in accumulate mode (old + new), against the
+    oracle; the saved tensor is the oracle's (kernel parity), contiguous like
+    a forward output, or the input view itself where the op saves its input."""
+    r = rng(seed_of("c2", name, layout))
     shape = (4096, 4096)
-    a = r.standard_normal(shape).astype(np.float32)
-    b = r.standard_normal(shape).astype(np.float32)
     g = r.standard_normal(shape).astype(np.float32)
-    xa, xb = _mk(a, layout), _mk(b, layout)
-    got = host(nt.Tensor._new_contiguous(K.binary(_lib.MUL, xa, xb), shape))
-    assert_bitexact(got, O.binary(O.MUL, a, b), "mul fwd 2^24")
+    tg = dev(g)
+    if name in ("add", "sub", "mul", "div"):
+        op, oop = {"add": (_lib.ADD, O.ADD), "sub": (_lib.SUB, O.SUB),
+                   "mul": (_lib.MUL, O.MUL), "div": (_lib.DIV, O.DIV)}[name]
+        a = r.standard_normal(shape).astype(np.float32)
+        b = (r.uniform(0.5, 2, shape) if name == "div" else r.standard_normal(shape)).astype(np.float32)
+        xa, xb = _mk(a, layout), _mk(b, layout)
+        got = host(nt.Tensor._new_contiguous(K.binary(op, xa, xb), shape))
+        assert_bitexact(got, O.binary(oop, a, b), f"{name} fwd 2^24 {layout}")
+        olds = [r.standard_normal(shape).astype(np.float32) for _ in range(2)]
+        tgts = [_mk(o, layout) for o in olds]
+        K.binary_bwd(op, tg, xa, xb, True, tgts[0], True, tgts[1])
+        for i, w in enumerate(O.bwd_binary(oop, g, a, b)):
+            want = O.accumulate(olds[i], w)
+            if name == "div" and i == 1:
+                scale = np.abs(w).astype(np.float64) + np.abs(olds[i])
+                assert_rel(host(tgts[i]), want, 1e-6, f"div grad 1 2^24 {layout}", scale=scale)
+            else:
+                assert_bitexact(host(tgts[i]), want, f"{name} grad {i} 2^24 {layout}")
+        return
+    op, oop, chain, dom, saved = C2_UNARY[name]
+    e = 2.5 if name == "pow" else 0.0
+    x = _inputs(r, dom, shape)
+    xx = _mk(x, layout)
+    got = host(nt.Tensor._new_contiguous(K.unary(op, xx, e), shape))
+    want_y = O.unary(oop, x, e) if oop is not None else O.unary(O.NEG, x)
+    if name in ("neg", "relu", "sqrt"):
+        assert_bitexact(got, want_y, f"{name} fwd 2^24 {layout}")
+    else:
+        assert_rel(got, want_y, 1e-6, f"{name} fwd 2^24 {layout}")
+    s = None if saved == "none" else (x if saved == "in" else want_y)
+    sv = None if s is None else (xx if saved == "in" else dev(s))
+    new = chain(g, s)
     old = r.standard_normal(shape).astype(np.float32)
-    tgt = dev(old)
-    K.binary_bwd(_lib.MUL, dev(g), xa, xb, True, tgt, False, None)
-    assert_bitexact(host(tgt), O.accumulate(old, O.binary(O.MUL, b, g)), "mul bwd 2^24")
-    got = host(nt.Tensor._new_contiguous(K.unary(_lib.TANH, xa), shape))
-    assert_rel(got, O.unary(O.TANH, a), 1e-6, "tanh 2^24")
+    tgt = _mk(old, layout)
+    K.unary_bwd(op, tg, sv, e, tgt)
+    want = O.accumulate(old, new)
+    if name in ("pow", "log", "sqrt", "tanh"):
+        scale = np.abs(new).astype(np.float64)
+        if name == "tanh":
+            scale = np.abs(g).astype(np.float64) * (1 + s.astype(np.float64) ** 2)
+        assert_rel(host(tgt), want, 1e-6, f"{name} bwd 2^24 {layout}", scale=scale + np.abs(old))
+    else:
+        assert_bitexact(host(tgt), want, f"{name} bwd 2^24 {layout}")
 
 
 # ------------------------------------------------- pow exponent fast paths

@@ -110,3 +110,31 @@ def test_gather_scatter_past_2_31():
     x[[BIG - 1, 2**31]] = nt.tensor([4.0, 6.0]).to("cuda")
     assert at(x, BIG - 1) == 4.0 and at(x, 2**31) == 6.0
     assert nt.sum(x).cpu().item() == 19.0
+
+
+def test_unaligned_flat_view_past_2_32():
+    # x[1:] of 2^32 + 9 elements: a view whose start is not 16-byte aligned
+    # takes the flat path one element per work-item, over more elements
+    # than one dispatch can hold (launched in chunks)
+    n = 2**32 + 9
+    x = nt.full(n, value=1.0, device="cuda")
+    x[2**32 + 3] = 5.0
+    x[2**30 + 1] = -2.0
+    y = -x[1:]
+    assert y.shape == (n - 1,)
+    assert at(y, 0) == -1.0
+    assert at(y, 2**30) == 2.0
+    assert at(y, 2**32 + 2) == -5.0
+    assert at(y, n - 2) == -1.0
+    assert at(y, 2**30 * 3 + 7) == -1.0
+
+
+def test_fill_past_64_gib():
+    # 2^34 + 12 fp32 (64 GiB + 48 B): more 16-byte words than one dispatch
+    # of the fill kernel holds, so its grid-stride loop takes the rest
+    n = 2**34 + 12
+    x = nt.full(n, value=3.0, device="cuda")
+    assert at(x, 0) == 3.0
+    assert at(x, 2**32 * 4 - 1) == 3.0
+    assert at(x, n - 1) == 3.0
+    assert at(x, n - 13) == 3.0

@@ -2,9 +2,9 @@
 oracle's sequential dot products.
 
 Bar: |gpu - ref| <= 1e-4 * (|A|.|B|)_ij per element (a different fp32
-accumulation order), plus a normwise check.  Small problems are compared in
-full; the config shapes are compared on sampled output elements (each a
-full-length sequential dot product in the oracle).
+accumulation order), plus a normwise check, on every output element; the
+config shapes against the oracle's OpenMP product (bit-identical to its
+sequential k loop).
 """
 
 from __future__ import annotations
@@ -93,41 +93,41 @@ def test_matmul_accumulate(gpu):
     assert_rel(host(tgt), want, 1e-4, "accumulate", scale=scale)
 
 
-def _sampled_check(got, A, B, r, what, n=256):
-    """Compare n random output elements against sequential dot products."""
-    M, N = got.shape
-    ii = r.integers(0, M, n)
-    jj = r.integers(0, N, n)
-    rows = np.ascontiguousarray(A[ii, :])
-    cols = np.ascontiguousarray(B[:, jj])
-    # oracle: sequential k loop per output, float32
-    want = np.array([O.matmul(rows[k:k + 1], cols[:, k:k + 1])[0, 0] for k in range(n)],
-                    dtype=np.float32)
-    scale = np.array([np.abs(rows[k]).astype(np.float64) @ np.abs(cols[:, k]).astype(np.float64)
-                      for k in range(n)])
-    assert_rel(got[ii, jj], want, 1e-4, what, scale=scale)
+def _full_check(got, want, scale, what):
+    """Every output: |gpu - ref| <= 1e-4 * (|A|.|B|)_ij, and normwise."""
+    assert_rel(got, want, 1e-4, what, scale=scale)
+    nrm = np.linalg.norm(got.astype(np.float64) - want) / max(np.linalg.norm(want), 1e-30)
+    assert nrm < 1e-5, (what, nrm)
 
 
 @pytest.mark.parametrize("M,K_,N", [(4096, 4096, 4096), (8192, 1024, 4096)])
 def test_config4_full_size(gpu, M, K_, N):
-    """Forward, dA = dG.B^T and dB = A^T.dG at the config shapes, through
-    autograd (MatmulOp), with A also given as a transposed view."""
+    """Config 4 at its shapes: forward, dA = dG.B^T and dB = A^T.dG through
+    autograd (MatmulOp), with A contiguous and as a transposed view.  Every
+    output element is compared with the oracle's sequential fp32 dot product
+    (the reference's k loop) within 1e-4 * (|A|.|B|)_ij."""
     r = rng(seed_of("c4", M, K_, N))
     A = r.standard_normal((M, K_)).astype(np.float32)
     B = (r.standard_normal((K_, N)) / np.sqrt(K_)).astype(np.float32)
     G = r.standard_normal((M, N)).astype(np.float32)
+    At, Bt = np.ascontiguousarray(A.T), np.ascontiguousarray(B.T)
+    aA, aB, aG = (np.abs(v).astype(np.float64) for v in (A, B, G))
+    ref = {"fwd": (O.matmul(A, B, parallel=True), aA @ aB),
+           "dA": (O.matmul(G, Bt, parallel=True), aG @ aB.T),
+           "dB": (O.matmul(At, G, parallel=True), aA.T @ aG)}
+    del aA, aB, aG
     for a_layout in ("contig", "transposed"):
         xa = dev(A) if a_layout == "contig" else dev_T(A)
-        xa = xa.to("cuda")
         xa.enable_grad()
         xb = dev(B, requires_grad=True)
         y = xa @ xb
-        _sampled_check(host(y), A, B, r, f"fwd {a_layout}")
+        _full_check(host(y), *ref["fwd"], f"fwd {a_layout} {M}x{K_}x{N}")
         # backward with upstream G: loss = sum(y * G) has dL/dy = G
         loss = (y * dev(G)).sum()
         loss.backward()
-        _sampled_check(host(xa.grad), G, np.ascontiguousarray(B.T), r, f"dA {a_layout}")
-        _sampled_check(host(xb.grad), np.ascontiguousarray(A.T), G, r, f"dB {a_layout}")
+        _full_check(host(xa.grad), *ref["dA"], f"dA {a_layout} {M}x{K_}x{N}")
+        _full_check(host(xb.grad), *ref["dB"], f"dB {a_layout} {M}x{K_}x{N}")
+        del xa, xb, y, loss
 
 
 def _batched_T(a):
@@ -157,19 +157,23 @@ def test_wide_tile_kernel_full_check(gpu, layout):
     assert_rel(host(tgt), want, 1e-4, f"wide accumulate {layout}", scale=scale)
 
 
+@pytest.mark.parametrize("layout", ["NN", "TN", "NT", "TT"])
 @pytest.mark.parametrize("accumulate", [False, True])
-def test_wide_tile_split_k_full_check(gpu, accumulate):
+def test_wide_tile_split_k_full_check(gpu, accumulate, layout):
     """[1024, 8192] @ [8192, 2048]: 32 tiles of 256x256, so the wide kernel
     splits K into 8 slices (one tile per CU) and sums them in slice order;
-    every output compared with an fp64 product (the bound covers fp32
-    accumulation in any order)."""
-    r = rng(seed_of("splitk", accumulate))
+    every operand layout (TN is the dB = A^T.dG of autograd); every output
+    compared with an fp64 product (the bound covers fp32 accumulation in any
+    order)."""
+    r = rng(seed_of("splitk", accumulate, layout))
     M, K_, N = 1024, 8192, 2048
     a = r.standard_normal((M, K_)).astype(np.float32)
     b = (r.standard_normal((K_, N)) / np.sqrt(K_)).astype(np.float32)
     old = r.standard_normal((M, N)).astype(np.float32)
     tgt = dev(old)
-    K.matmul_into(dev(a), dev(b), tgt, accumulate=accumulate)
+    xa = dev_T(a) if layout[0] == "T" else dev(a)
+    xb = dev_T(b) if layout[1] == "T" else dev(b)
+    K.matmul_into(xa, xb, tgt, accumulate=accumulate)
     want = a.astype(np.float64) @ b.astype(np.float64) + (old if accumulate else 0.0)
     scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64) + (
         np.abs(old) if accumulate else 0.0)

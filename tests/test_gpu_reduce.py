@@ -177,20 +177,53 @@ def test_mean_backward(gpu, acc):
 
 @pytest.mark.parametrize("axes", [(0,), (1,), (0, 1)])
 def test_config3_full_size(gpu, axes):
-    """[8192, 8192] fp32: sum within the condition-aware bound, max value /
-    index bit-exact, max backward routing bit-exact."""
+    """Config 3 at its size, [8192, 8192] fp32 ~ N(0,1), along axis 0, axis 1
+    and the full tensor: sum and mean within the condition-aware bound; max
+    and min values, argmax / argmin indices and tie counts bit-exact; the
+    backward of sum and mean (accumulate: old + broadcast(g) and
+    old + broadcast(g) / n) bit-exact; max and min backward routing (first
+    write and accumulate) bit-exact."""
     r = rng(seed_of("c3", axes))
     shape = (8192, 8192)
     a = r.standard_normal(shape).astype(np.float32)
     x = dev(a)
     kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+    k = int(np.prod(kshape))
+    n = a.size // k
+    bound = _sum_bound(a, axes)
     got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, axes, nt.float32), kshape))
     want = O.reduce(O.R_SUM, a, axes, np.float32)
-    assert_rel(got, want, 1e-5, "sum 2^26", scale=_sum_bound(a, axes))
-    v, idx, cnt = K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True)
-    assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), O.reduce(O.R_MAX, a, axes), "max 2^26")
-    assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(O.R_ARGMAX, a, axes), "argmax 2^26")
-    if axes != (0, 1):
-        g = r.standard_normal(kshape).astype(np.float32)
-        st = K.reduce_bwd(_lib.R_MAX, dev(g), 1.0, idx, cnt, axes, shape, None)
-        assert_bitexact(host(nt.Tensor._new_contiguous(st, shape)), O.sel_bwd(O.R_MAX, g, a, axes), "max bwd 2^26")
+    assert_rel(got, want, 1e-5, "sum 2^26", scale=bound)
+    # mean (ops_reduction.py:119-127): sum / float32(n), through the API
+    got = host(nt.mean(x, axis=axes))
+    assert_rel(got, O.mean_fwd(a, axes), 1e-5, "mean 2^26", scale=bound / n)
+    g = r.standard_normal(kshape).astype(np.float32)
+    gshape = tuple(1 if i in axes else s for i, s in enumerate(shape))
+    gb = np.broadcast_to(g.reshape(gshape), shape)
+    for op, oop, aop, name in ((_lib.R_MAX, O.R_MAX, O.R_ARGMAX, "max"),
+                               (_lib.R_MIN, O.R_MIN, O.R_ARGMIN, "min")):
+        v, idx, cnt = K.reduce(op, x, axes, nt.float32, want_aux=True)
+        assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), O.reduce(oop, a, axes), f"{name} 2^26")
+        assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(aop, a, axes),
+                        f"arg{name} 2^26")
+        ext = O.reduce(oop, a, axes).reshape(gshape)
+        want_cnt = (a == ext).sum(axis=axes).astype(np.int32).reshape(kshape)
+        assert_bitexact(host(nt.Tensor._new_contiguous(cnt, kshape)), want_cnt, f"{name} count 2^26")
+        want = O.sel_bwd(oop, g, a, axes)
+        st = K.reduce_bwd(op, dev(g), 1.0, idx, cnt, axes, shape, None)
+        assert_bitexact(host(nt.Tensor._new_contiguous(st, shape)), want, f"{name} bwd 2^26")
+        old = r.standard_normal(shape).astype(np.float32)
+        tgt = dev(old)
+        K.reduce_bwd(op, dev(g), 1.0, idx, cnt, axes, shape, tgt)
+        assert_bitexact(host(tgt), O.accumulate(old, want), f"{name} bwd acc 2^26")
+    # sum backward (ops_reduction.py:67-74): broadcast(g), accumulated
+    old = r.standard_normal(shape).astype(np.float32)
+    tgt = dev(old)
+    K.inplace(_lib.ADD, tgt, dev(g).reshape(*gshape).expand(*shape))
+    assert_bitexact(host(tgt), O.accumulate(old, np.ascontiguousarray(gb)), "sum bwd acc 2^26")
+    # mean backward (:129-138): broadcast(g) / float32(n), accumulated
+    old = r.standard_normal(shape).astype(np.float32)
+    tgt = dev(old)
+    K.reduce_bwd(_lib.R_MEAN, dev(g), float(n), None, None, axes, shape, tgt)
+    want = O.binary(O.DIV, gb, np.broadcast_to(O.scalar(n, np.float32), shape))
+    assert_bitexact(host(tgt), O.accumulate(old, want), "mean bwd acc 2^26")

@@ -410,3 +410,46 @@ def test_rng_oracle_pinned():
     lo, hi = np.float32(-2.5), np.float32(7.0)
     base = O.uniform(9, 50)
     assert O.uniform(9, 50, low=-2.5, high=7.0).tobytes() == (base * (hi - lo) + lo).tobytes()
+
+
+def test_sequential_sum_bias_of_long_positive_sums():
+    """The reference's sum (reduction_ops.cu:63-69) adds left to right in
+    fp32.  Closed form: 2^25 ones sum to exactly 2^24 (past 2^24, adding 1
+    is a tie that rounds back to even), so the reference's mean of 2^25 ones
+    is 0.5.  The oracle equals numpy's left-to-right float32 accumulation on
+    config 5's loss shape (8192 x 1000 squared N(0, 1.6) errors), and that
+    reads below the float64 sum by more than 0.5%: the reference's config-5
+    loss carries this summation error, the GPU's tree sum does not."""
+    ones = np.ones(2**25, dtype=np.float32)
+    assert float(O.reduce(O.R_SUM, ones, (0,))) == 2.0**24
+    assert float(O.mean_fwd(ones, (0,))) == 0.5
+    r = np.random.default_rng(7)
+    sq = (r.standard_normal((8192, 1000)) * 1.6).astype(np.float32) ** 2
+    seq = np.add.accumulate(sq.ravel(), dtype=np.float32)[-1]
+    got = O.reduce(O.R_SUM, sq, (0, 1))
+    assert got.view(np.uint32) == np.float32(seq).view(np.uint32)
+    exact = sq.astype(np.float64).sum()
+    assert (exact - float(got)) / exact > 5e-3
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1, 1), (5, 7, 3), (67, 300, 129), (128, 513, 320),
+                                   (4, 256, 64), (3, 2, 70), (130, 257, 260)])
+def test_blocked_openmp_matmul_bit_identical(M, K, N):
+    """or_matmul_omp (cache-blocked i-k-j, vectorised, OpenMP) against the
+    reference's loop order (or_matmul), bit for bit, with signed zeros in
+    the operands (0 + (-0) is +0 in both orders), ragged block edges and a
+    transposed view."""
+    r = np.random.default_rng(M * 1000 + K)
+    a = r.standard_normal((M, K)).astype(np.float32)
+    b = r.standard_normal((K, N)).astype(np.float32)
+    a[a > 1.5] = -0.0
+    b[b > 1.5] = 0.0
+    want = O.matmul(a, b)
+    assert np.array_equal(O.matmul(a, b, parallel=True).view(np.uint32), want.view(np.uint32))
+    at = np.ascontiguousarray(a.T).T
+    assert np.array_equal(O.matmul(at, b, parallel=True).view(np.uint32), want.view(np.uint32))
+    A = r.standard_normal((2, 3, M, K)).astype(np.float32)
+    Bb = np.broadcast_to(b, (2, 3, K, N))
+    assert np.array_equal(O.matmul(A, Bb, parallel=True), O.matmul(A, Bb))
+    d, e = a.astype(np.float64), b.astype(np.float64)
+    assert np.array_equal(O.matmul(d, e, parallel=True), O.matmul(d, e))
