@@ -221,6 +221,27 @@ int nt_binary_bwd(int32_t op, const nt_view *g, const nt_view *a,
 int nt_reduce(int32_t op, const nt_view *x, const int64_t *axes, int32_t naxes,
               const nt_view *out, const nt_view *idx, const nt_view *count);
 
+/* Bytes of the static device scratch array of the allocation-free entry
+ * points (one array per GPU, held until the process ends). */
+#define NT_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* nt_reduce without any allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, results and errors as nt_reduce; the partial results of
+ * multi-pass reductions go to the library's static scratch array of
+ * NT_NOALLOC_SCRATCH_BYTES instead of the caching allocator, and a
+ * reduction that would need more is rejected (NT_ERR_VALUE) -- every plan
+ * nt_reduce makes today fits (its largest partial set, max/min along axis 0
+ * of a wide tensor, is 8 MiB for fp32).  The library must be initialised
+ * first (nt_init or any other call): initialisation allocates, this entry
+ * point refuses to do it (NT_ERR_RUNTIME).  Calls that overlap on one GPU
+ * share the array and race; host-serialised calls on the library stream
+ * (the library's own ordering) do not. */
+int nt_reduce_noalloc(int32_t op, const nt_view *x, const int64_t *axes,
+                      int32_t naxes, const nt_view *out, const nt_view *idx,
+                      const nt_view *count);
+
 /* Backward of the reductions (src/nanotorch/autograd/ops_reduction.py:67-74,
  * 129-138, 201-212, 275-286), fused with the engine's accumulation:
  *   NT_SUM:  gx = g_s                        (broadcast over reduced axes)

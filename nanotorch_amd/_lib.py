@@ -74,6 +74,7 @@ _SIGNATURES = {
     "nt_unary_bwd": (c_int, [c_int32, _VP, _VP, c_double, _VP, c_int32]),
     "nt_binary_bwd": (c_int, [c_int32, _VP, _VP, _VP, _VP, c_int32, _VP, c_int32]),
     "nt_reduce": (c_int, [c_int32, _VP, POINTER(c_int64), c_int32, _VP, _VP, _VP]),
+    "nt_reduce_noalloc": (c_int, [c_int32, _VP, POINTER(c_int64), c_int32, _VP, _VP, _VP]),
     "nt_reduce_bwd": (
         c_int,
         [c_int32, _VP, c_double, _VP, _VP, POINTER(c_int64), c_int32, _VP, c_int32],

@@ -31,6 +31,10 @@ struct Error : std::exception {
 
 void set_last_error(const std::string &msg);
 void ensure_init();
+bool runtime_initialised();
+// Device address of the current GPU's static scratch array (bytes:
+// NT_NOALLOC_SCRATCH_BYTES), resolved when the library initialised.
+void *noalloc_scratch();
 hipStream_t stream();
 // Device pointer to the deferred-error word: a kernel that finds an invalid
 // argument it cannot report synchronously stores an nt_status there (plain
@@ -99,6 +103,19 @@ template <class F> int guard(F &&f) {
     set_last_error(e.what());
     return NT_ERR_RUNTIME;
   }
+}
+
+// guard() for the allocation-free entry points: the library must already be
+// initialised (initialisation creates the stream and allocates), so this
+// variant refuses to run instead of initialising.
+template <class F> int guard_initialised(F &&f) {
+  std::lock_guard<std::recursive_mutex> lock(api_mutex());
+  if (!runtime_initialised()) {
+    set_last_error("the library is not initialised: call nt_init() first "
+                   "(initialisation allocates; this entry point does not)");
+    return NT_ERR_RUNTIME;
+  }
+  return guard(std::forward<F>(f));
 }
 
 // ------------------------------------------------------------------ dtypes

@@ -544,8 +544,32 @@ KeepDesc to_keep_desc(const nt_view &v) {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Partial results of one reduction: from the caching allocator (nt_reduce),
+// or from the static scratch array whose device address `fixed` is
+// (nt_reduce_noalloc), checked against its size.  Every partial slot is
+// written by the first pass before the combine pass reads it, so the
+// array's earlier contents never matter.
+class PartialBuf {
+public:
+  PartialBuf(size_t nbytes, void *fixed)
+      : alloc_(fixed != nullptr ? 0 : nbytes) {
+    if (fixed != nullptr && nbytes > NT_NOALLOC_SCRATCH_BYTES)
+      fail(NT_ERR_VALUE, "reduction needs " + std::to_string(nbytes) +
+                             " bytes of partial results, more than the " +
+                             std::to_string(NT_NOALLOC_SCRATCH_BYTES) +
+                             "-byte allocation-free scratch");
+    p_ = fixed != nullptr ? (nbytes ? fixed : nullptr) : alloc_.get();
+  }
+  template <class T> T *get() const { return static_cast<T *>(p_); }
+
+private:
+  DeviceScratch alloc_;
+  void *p_;
+};
+
 template <class T, class O, class Acc, int MODE>
-void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
+void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out,
+                void *fixed) {
   if (p.K == 0)
     return;
   const T *xp = typed_ptr<const T>(x);
@@ -592,7 +616,7 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
     int64_t seg = ceil_div(p.D, S);
     seg = ceil_div(seg, VEC) * VEC;
     S = ceil_div(p.D, seg);
-    DeviceScratch partial_buf(S > 1 ? sizeof(Acc) * p.K * S : 0);
+    PartialBuf partial_buf(S > 1 ? sizeof(Acc) * p.K * S : 0, fixed);
     Acc *partial = partial_buf.get<Acc>();
     const KeepDesc kd = to_keep_desc(p.keep);
     const int64_t blocks = p.K * S;
@@ -635,7 +659,7 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
     S = std::min<int64_t>(S, 65535);
     const int64_t seg = ceil_div(D, S);
     S = ceil_div(D, seg);
-    DeviceScratch partial_buf(S > 1 ? sizeof(Acc) * K * S : 0);
+    PartialBuf partial_buf(S > 1 ? sizeof(Acc) * K * S : 0, fixed);
     Acc *partial = partial_buf.get<Acc>();
     if (bx >= (int64_t(1) << 31))
       fail(NT_ERR_RUNTIME, "reduction too large");
@@ -679,7 +703,7 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out) {
   S = std::max<int64_t>(1, std::min<int64_t>(S, 1 << 16));
   const int64_t seg = ceil_div(p.D, S);
   S = ceil_div(p.D, seg);
-  DeviceScratch partial_buf(S > 1 ? sizeof(Acc) * p.K * S : 0);
+  PartialBuf partial_buf(S > 1 ? sizeof(Acc) * p.K * S : 0, fixed);
   Acc *partial = partial_buf.get<Acc>();
   const int64_t blocks = p.K * S;
   if (blocks >= (int64_t(1) << 31))
@@ -868,11 +892,14 @@ template <class T, bool ACC> struct BcastBwd {
 
 using namespace nt;
 
-extern "C" {
+namespace {
 
-int nt_reduce(int32_t op, const nt_view *x, const int64_t *axes, int32_t naxes,
-              const nt_view *out, const nt_view *idx, const nt_view *count) {
-  return guard([&] {
+// nt_reduce's body; fixed: the static scratch's device address for the
+// allocation-free variant, nullptr to take partials from the allocator.
+void reduce_impl(int32_t op, const nt_view *x, const int64_t *axes,
+                 int32_t naxes, const nt_view *out, const nt_view *idx,
+                 const nt_view *count, void *fixed) {
+  {
     check_view(x, "reduction");
     check_view(out, "reduction");
     if (naxes < 0 || naxes > x->ndim)
@@ -892,7 +919,7 @@ int nt_reduce(int32_t op, const nt_view *x, const int64_t *axes, int32_t naxes,
                out->offset * int64_t(dtype_size(out->dtype));
       dispatch_all(x->dtype, [&]<class T>() {
         dispatch_arith(out->dtype, [&]<class O>() {
-          run_reduce<T, O, SumAcc<O>, 0>(x, p, ro);
+          run_reduce<T, O, SumAcc<O>, 0>(x, p, ro, fixed);
         });
       });
       return;
@@ -919,9 +946,9 @@ int nt_reduce(int32_t op, const nt_view *x, const int64_t *axes, int32_t naxes,
       }
       dispatch_all(x->dtype, [&]<class T>() {
         if (is_max)
-          run_reduce<T, T, SelAcc<T, true>, 1>(x, p, ro);
+          run_reduce<T, T, SelAcc<T, true>, 1>(x, p, ro, fixed);
         else
-          run_reduce<T, T, SelAcc<T, false>, 1>(x, p, ro);
+          run_reduce<T, T, SelAcc<T, false>, 1>(x, p, ro, fixed);
       });
       return;
     }
@@ -931,13 +958,31 @@ int nt_reduce(int32_t op, const nt_view *x, const int64_t *axes, int32_t naxes,
       RedOut<2> ro{typed_ptr<int64_t>(out), nullptr, nullptr};
       dispatch_all(x->dtype, [&]<class T>() {
         if (is_max)
-          run_reduce<T, T, SelAcc<T, true>, 2>(x, p, ro);
+          run_reduce<T, T, SelAcc<T, true>, 2>(x, p, ro, fixed);
         else
-          run_reduce<T, T, SelAcc<T, false>, 2>(x, p, ro);
+          run_reduce<T, T, SelAcc<T, false>, 2>(x, p, ro, fixed);
       });
       return;
     }
     fail(NT_ERR_VALUE, "reduction: unknown op");
+  }
+}
+
+} // namespace
+
+extern "C" {
+
+int nt_reduce(int32_t op, const nt_view *x, const int64_t *axes, int32_t naxes,
+              const nt_view *out, const nt_view *idx, const nt_view *count) {
+  return guard(
+      [&] { reduce_impl(op, x, axes, naxes, out, idx, count, nullptr); });
+}
+
+int nt_reduce_noalloc(int32_t op, const nt_view *x, const int64_t *axes,
+                      int32_t naxes, const nt_view *out, const nt_view *idx,
+                      const nt_view *count) {
+  return guard_initialised([&] {
+    reduce_impl(op, x, axes, naxes, out, idx, count, noalloc_scratch());
   });
 }
 

@@ -18,8 +18,21 @@ namespace {
 
 thread_local std::string g_last_error;
 
+// Scratch of the allocation-free entry points (nt_reduce_noalloc): one
+// static device array per GPU, held until the process ends.  Host code never
+// passes `scratch` itself to a kernel (on the host the name is a stand-in,
+// not a device address): set-up resolves its device address with
+// hipGetSymbolAddress, once per device, and every use goes through that
+// pointer.  Calls that overlap on one GPU share the array and race; the
+// reductions' partial results are written in full before they are read, so
+// nothing in it needs clearing between calls.
+static __device__ __align__(256) unsigned char scratch[NT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+
 struct Runtime {
   bool initialised = false;
+  void *scratch_ptr[MAX_DEVICES] = {};
   bool available = false;
   int cu_count = 0;
   hipStream_t stream = nullptr;
@@ -104,6 +117,13 @@ void ensure_init() {
     fail(NT_ERR_RUNTIME, "no HIP device available");
   }
   NT_HIP_CHECK(hipSetDevice(0));
+  // The static scratch array's address on this device (it may load the
+  // library's code object, so it is done here, not in the entry point).
+  void *sp = nullptr;
+  NT_HIP_CHECK(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+  if (sp == nullptr)
+    fail(NT_ERR_RUNTIME, "no device address for the static scratch array");
+  r.scratch_ptr[0] = sp;
   hipDeviceProp_t prop;
   NT_HIP_CHECK(hipGetDeviceProperties(&prop, 0));
   r.cu_count = prop.multiProcessorCount;
@@ -129,6 +149,16 @@ bool ew_nontemporal() {
 }
 
 hipStream_t stream() { return rt().stream; }
+bool runtime_initialised() { return rt().initialised; }
+
+void *noalloc_scratch() {
+  int dev = 0;
+  NT_HIP_CHECK(hipGetDevice(&dev));
+  void *p = (dev >= 0 && dev < MAX_DEVICES) ? rt().scratch_ptr[dev] : nullptr;
+  if (p == nullptr)
+    fail(NT_ERR_RUNTIME, "static scratch not set up on the current device");
+  return p;
+}
 int *deferred_error_word() { return rt().deferred_dev; }
 
 void raise_deferred_error() {

@@ -48,3 +48,16 @@ def test_view_struct_layout():
     # struct nt_view: void*, int64, int32, int32, int64[8], int64[8]
     assert ctypes.sizeof(_lib.NtView) == 8 + 8 + 4 + 4 + 64 + 64
     assert _lib.NtView.shape.offset == 24
+
+
+def test_noalloc_entry_point_refuses_before_init():
+    """nt_reduce_noalloc never initialises the library (initialisation
+    allocates): before any other call it returns NT_ERR_RUNTIME."""
+    lib = _lib.load()
+    avail = ctypes.c_int(0)
+    lib.nt_is_available(ctypes.byref(avail))
+    if avail.value:
+        return  # a GPU process may have initialised the library already
+    rc = lib.nt_reduce_noalloc(0, None, None, 0, None, None, None)
+    assert rc == _lib.NT_ERR_RUNTIME
+    assert b"nt_init" in lib.nt_last_error()
