@@ -580,57 +580,189 @@ def bench_copy_reference(iters: int = 8) -> dict:
 # ------------------------------------------------------------ CPU baseline
 
 
-def cpu_baseline(rows: int = 1024) -> dict:
-    """The oracle (reference CPU kernels restated, single thread) on a
-    [rows, 4096] sample of the config-2 sweep: forward, then the reference's
-    backward composition and the engine's accumulate, both layouts."""
+def _host_cpu() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn) -> float:
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
+
+
+def cpu_per_op(rows: int = 512) -> dict:
+    """ref-cpu-1t: the oracle (the reference's CPU kernels and Python
+    backward compositions, restated; single thread, as the reference has no
+    threads) timed per op on bounded samples of configs 2-5, with the GPU
+    figures' byte / FLOP models, so that every GPU per-kernel figure has a
+    CPU figure beside it.
+
+    config 2: [rows, 4096] (rows/4096 of the workload), each op's forward and
+      its backward composition plus the engine's accumulate, both layouts
+      (the transposed sample is the .T view of a contiguous [4096, rows]);
+    config 3: [512, 8192] (1/16 of the rows), sum / max / min forward and
+      sum (accumulate) / mean / max backward along axis 0, axis 1 and all;
+    config 4: 2 output rows of each product (fwd, dA = dG.B^T, dB = A^T.dG,
+      with A contiguous and as a .T view; dA does not read A), the
+      reference's k loop per output, with the whole product's time
+      extrapolated linearly in rows;
+    config 5: one training step of the 4-layer network at batch 4, and the
+      SGD update alone; the rest of the step is linear in the batch, so the
+      step at batch 8192 is estimated as update + (step - update) * 2048."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
     r = np.random.default_rng(7)
+    out: dict = {"elementwise": {}, "reductions": {}, "matmul": {}, "mlp": {}}
+    # ---- config 2
     shape = (rows, 4096)
     n = rows * 4096
-    total_bytes = 0
-    t0 = time.perf_counter()
+    tot_b = tot_s = 0.0
     for layout in ("contig", "transposed"):
         mk = (lambda a: a) if layout == "contig" else (lambda a: np.ascontiguousarray(a.T).T)
         for name, op in (("add", O.ADD), ("sub", O.SUB), ("mul", O.MUL), ("truediv", O.DIV)):
             a = mk(r.standard_normal(shape).astype(np.float32))
             b = mk((r.uniform(0.5, 2, shape) if name == "truediv" else r.standard_normal(shape)).astype(np.float32))
             g = r.standard_normal(shape).astype(np.float32)
-            O.binary(op, a, b)
-            ga, gb = O.bwd_binary(op, g, a, b)
-            O.accumulate(np.ones(shape, np.float32), ga)
-            O.accumulate(np.ones(shape, np.float32), gb)
-            total_bytes += (ew_bytes(name, "fwd") + ew_bytes(name, "bwd")) * n // N_ELEM
+            olds = [mk(r.standard_normal(shape).astype(np.float32)) for _ in range(2)]
+            tf = _timed(lambda: O.binary(op, a, b))
+
+            def bwd():
+                ga, gb = O.bwd_binary(op, g, a, b)
+                O.inplace(O.ADD, olds[0], ga)
+                O.inplace(O.ADD, olds[1], gb)
+            tb = _timed(bwd)
+            for phase, t in (("fwd", tf), ("bwd", tb)):
+                nb = ew_bytes(name, phase) * n // N_ELEM
+                out["elementwise"][f"{name}|{layout}|{phase}"] = round(nb / t / 1e9, 3)
+                tot_b += nb
+                tot_s += t
         for name, op, dom, saved, e in UNARY_OPS:
             x = mk((r.standard_normal(shape) if dom is None else r.uniform(dom[0], dom[1], shape)).astype(np.float32))
             g = r.standard_normal(shape).astype(np.float32)
+            old = mk(r.standard_normal(shape).astype(np.float32))
             oop = {"neg": O.NEG, "exp": O.EXP, "log": O.LOG, "sqrt": O.SQRT, "pow": O.POW,
                    "relu": O.RELU, "sigmoid": O.SIGMOID, "tanh": O.TANH}[name]
-            y = O.unary(oop, x, e)
+            y = None
+
+            def fwd():
+                nonlocal y
+                y = O.unary(oop, x, e)
+            tf = _timed(fwd)
             chain = {"neg": lambda: O.bwd_neg(g), "exp": lambda: O.bwd_exp(g, y),
                      "log": lambda: O.bwd_log(g, x), "sqrt": lambda: O.bwd_sqrt(g, y),
                      "pow": lambda: O.bwd_pow(g, x, 2.5), "relu": lambda: O.bwd_relu(g, y),
                      "sigmoid": lambda: O.bwd_sigmoid(g, y), "tanh": lambda: O.bwd_tanh(g, y)}[name]
-            O.accumulate(np.ones(shape, np.float32), chain())
-            total_bytes += (ew_bytes(name, "fwd") + ew_bytes(name, "bwd")) * n // N_ELEM
-    dt = time.perf_counter() - t0
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": round(total_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": f"config-2 sweep on [{rows},4096] (1/{4096 // rows} of the workload), "
-                      f"forward + reference backward composition + accumulate, both layouts, "
-                      f"single thread, {dt:.1f} s",
-            "host_cpu": cpu, "host_nproc": os.cpu_count()}
+            tb = _timed(lambda: O.inplace(O.ADD, old, chain()))
+            for phase, t in (("fwd", tf), ("bwd", tb)):
+                nb = ew_bytes(name, phase) * n // N_ELEM
+                out["elementwise"][f"{name}|{layout}|{phase}"] = round(nb / t / 1e9, 3)
+                tot_b += nb
+                tot_s += t
+    out["elementwise_sample"] = f"[{rows}, 4096] (1/{4096 // rows} of config 2)"
+    baseline = {"value": round(tot_b / tot_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"config-2 sweep on [{rows},4096] (1/{4096 // rows} of the workload), "
+                          f"forward + reference backward composition + accumulate, both layouts, "
+                          f"single thread, {tot_s:.1f} s",
+                "host_cpu": _host_cpu(), "host_nproc": os.cpu_count()}
+    # ---- config 3
+    x = r.standard_normal((512, 8192)).astype(np.float32)
+    nx = x.size
+    for label, axes in (("axis0", (0,)), ("axis1", (1,)), ("full", (0, 1))):
+        kshape = tuple(s_ for i, s_ in enumerate(x.shape) if i not in axes)
+        gshape = tuple(1 if i in axes else s_ for i, s_ in enumerate(x.shape))
+        for name, op in (("sum", O.R_SUM), ("max", O.R_MAX), ("min", O.R_MIN)):
+            t = _timed(lambda: O.reduce(op, x, axes, np.float32 if op == O.R_SUM else None))
+            out["reductions"][f"{name}|{label}|fwd"] = round(nx * 4 / t / 1e9, 3)
+        g = r.standard_normal(kshape).astype(np.float32)
+        gb = np.broadcast_to(g.reshape(gshape), x.shape)
+        old = r.standard_normal(x.shape).astype(np.float32)
+        t = _timed(lambda: O.inplace(O.ADD, old, gb))  # engine: grad += expand(g)
+        out["reductions"][f"sum|{label}|bwd"] = round(2 * nx * 4 / t / 1e9, 3)
+        dn = nx // max(1, int(np.prod(kshape)))
+        t = _timed(lambda: O.binary(O.DIV, gb, np.broadcast_to(O.scalar(dn, np.float32), x.shape)))
+        out["reductions"][f"mean|{label}|bwd"] = round(nx * 4 / t / 1e9, 3)
+        t = _timed(lambda: O.sel_bwd(O.R_MAX, g, x, axes))
+        out["reductions"][f"max|{label}|bwd"] = round(nx * 4 / t / 1e9, 3)
+    out["reductions_sample"] = "[512, 8192] fp32 (1/16 of config 3)"
+    # ---- config 4
+    rs = 2
+    for (M, Kd, N) in ((4096, 4096, 4096), (8192, 1024, 4096)):
+        A = r.standard_normal((M, Kd)).astype(np.float32)
+        B = (r.standard_normal((Kd, N)) / np.sqrt(Kd)).astype(np.float32)
+        G = r.standard_normal((M, N)).astype(np.float32)
+        At = np.ascontiguousarray(A.T).T  # A as the .T view of a [K, M] storage
+        for a_layout, AA in (("contig", A), ("transposed", At)):
+            entry = {}
+            for name, x1, x2, full_rows, (m_, k_, n_) in (
+                    ("fwd", AA[:rs], B, M, (M, Kd, N)),
+                    ("dA", G[:rs], B.T, M, (M, N, Kd)),
+                    ("dB", AA[:, :rs].T, G, Kd, (Kd, M, N))):
+                if name == "dA" and a_layout == "transposed":
+                    entry[name] = out["matmul"][f"{M}x{Kd}x{N}|contig"][name]  # same operands
+                    continue
+                t = _timed(lambda: O.matmul(x1, x2))
+                gf = 2.0 * rs * k_ * n_ / t / 1e9
+                entry[name] = {"GFLOP/s": round(gf, 3),
+                               "full_product_s_extrapolated": round(t * full_rows / rs, 1)}
+            out["matmul"][f"{M}x{Kd}x{N}|{a_layout}"] = entry
+    out["matmul_sample"] = f"{rs} output rows per product, extrapolated linearly"
+    # ---- config 5: one step at batch 4, split into its batch-independent
+    # part (the SGD update of all 41.9 M parameters, timed on its own) and a
+    # per-sample part (everything else is linear in the batch)
+    bsz = 4
+    xb = r.standard_normal((bsz, C5_DIMS[0])).astype(np.float32)
+    tb_ = r.standard_normal((bsz, C5_DIMS[-1])).astype(np.float32)
+    params = [((r.standard_normal((C5_DIMS[i], C5_DIMS[i + 1])) * np.sqrt(2.0 / C5_DIMS[i])).astype(np.float32),
+               np.zeros(C5_DIMS[i + 1], np.float32)) for i in range(4)]
+    t_step = _timed(lambda: O.mlp_step(params, xb, tb_, C5_ACTS, C5_LR, parallel=False))
+
+    def sgd():  # optimizers.py:51, p -= p.grad * lr, on gradient-sized arrays
+        for W, b in params:
+            O.inplace(O.SUB, W, O.mul_scalar(W, C5_LR))
+            O.inplace(O.SUB, b, O.mul_scalar(b, C5_LR))
+    t_sgd = min(t_step, _timed(sgd))
+    full = t_sgd + (t_step - t_sgd) * C5_BATCH / bsz
+    out["mlp"] = {"step_s_at_batch_4": round(t_step, 3), "sgd_update_s": round(t_sgd, 3),
+                  "step_s_extrapolated_batch_8192": round(full, 1),
+                  "step/s_extrapolated": round(1.0 / full, 6)}
+    out["threads"] = 1
+    out["host_cpu"] = _host_cpu()
+    out["host_nproc"] = os.cpu_count()
+    return {"baseline": baseline, "per_op": out}
+
+
+def attach_cpu(parts: dict, cpu: dict) -> None:
+    """Writes each CPU figure next to the matching GPU per-kernel figure
+    (same key and byte / FLOP model) and the GPU/CPU ratio."""
+    ew = parts.get("elementwise_per_kernel", {})
+    for k, v in cpu["elementwise"].items():
+        if k in ew:
+            ew[k]["cpu_1t_GB/s"] = v
+            ew[k]["gpu_over_cpu"] = round(ew[k]["GB/s"] / v, 1)
+    red = parts.get("reductions", {}).get("per_kernel", {})
+    for k, v in cpu["reductions"].items():
+        if k in red:
+            red[k]["cpu_1t_GB/s"] = v
+            red[k]["gpu_over_cpu"] = round(red[k]["GB/s"] / v, 1)
+    mm = parts.get("matmul", {})
+    for k, ent in cpu["matmul"].items():
+        for name, v in ent.items():
+            if k in mm and name in mm[k]:
+                mm[k][name]["cpu_1t_GFLOP/s"] = v["GFLOP/s"]
+                mm[k][name]["cpu_1t_full_product_s"] = v["full_product_s_extrapolated"]
+                mm[k][name]["gpu_over_cpu"] = round(mm[k][name]["TFLOP/s"] * 1e3 / v["GFLOP/s"], 0)
+    if "mlp" in parts and cpu.get("mlp"):
+        parts["mlp"]["cpu_1t_step_s_extrapolated"] = cpu["mlp"]["step_s_extrapolated_batch_8192"]
+        parts["mlp"]["gpu_over_cpu"] = round(
+            cpu["mlp"]["step_s_extrapolated_batch_8192"] / (parts["mlp"]["ms_per_step"] * 1e-3), 0)
 
 
 def cpu_parts() -> dict:
@@ -652,7 +784,7 @@ def cpu_parts() -> dict:
             dt_s = time.perf_counter() - t0
             red[f"{name}|{label}|fwd"] = round(x.nbytes / dt_s / 1e9, 3)
     out["reductions_GB/s_1thread"] = red
-    out["reductions_sample"] = "[1024, 8192] fp32 (1/8 of config 3)"
+    out["reductions_sample"] = "[512, 8192] fp32 (1/16 of config 3)"
     # config 4 sample: 512^3 single thread, 1024^3 on all cores
     mm = {}
     for n, par in ((512, False), (1024, True)):
@@ -941,8 +1073,14 @@ def main() -> int:
     if "next" in parts:
         line["parts"]["next_rows"] = bench_next()
     if "cpu" in parts:
-        line["cpu_baseline"] = cpu_baseline()
+        cpu = cpu_per_op()
+        line["cpu_baseline"] = cpu["baseline"]
+        attach_cpu(line["parts"], cpu["per_op"])
         line["parts"]["cpu_reference"] = cpu_parts()
+        line["parts"]["cpu_reference"]["per_op_samples"] = {
+            k: cpu["per_op"][k] for k in ("elementwise_sample", "reductions_sample", "matmul_sample",
+                                          "threads", "host_cpu", "host_nproc")}
+        line["parts"]["cpu_reference"]["mlp_config5"] = cpu["per_op"]["mlp"]
     else:
         line["cpu_baseline"] = None
     line["host"] = platform.node()

@@ -57,8 +57,14 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 #ifndef NT_COL_WG_SUM
 #define NT_COL_WG_SUM 1
 #endif
+// Max/min column walks issue the next UR rows' loads before the current
+// rows' selects (measured on [8192, 8192] axis 0: 0.60 -> 0.675 of peak at one
+// workgroup per CU; without it two workgroups per CU were best).
+#ifndef NT_COL_PIPE
+#define NT_COL_PIPE 1
+#endif
 #ifndef NT_COL_WG_SEL
-#define NT_COL_WG_SEL 2 // measured: max/min axis 0 4.3 / 5.0 / 4.6 / 4.0 TB/s at 1 / 2 / 4 / 8
+#define NT_COL_WG_SEL 1 // measured with NT_COL_PIPE: 0.675 / 0.51 of peak at 1 / 2
 #endif
 
 // ------------------------------------------------------------ accumulators
@@ -92,17 +98,26 @@ template <class O, bool IS_MAX> struct SelAcc {
     else
       return a < b;
   }
+  __device__ __forceinline__ static bool better_eq(O a, O b) {
+    if constexpr (IS_MAX)
+      return a >= b;
+    else
+      return a <= b;
+  }
   // Branch-free update (selects, no divergent control flow).  Every kernel
   // feeds an accumulator its elements in increasing j, so on a tie the
   // stored, earlier index stays -- unless nothing equal has been counted yet
   // (c == 0: the neutral value with index INT64_MAX met an element equal to
-  // it), when the element's index is the first.
+  // it), when the element's index is the first.  In one expression: the
+  // new count is 1 exactly when the element is better, or equal with
+  // nothing counted, and that is when its index is taken (x >= v and the
+  // new count is 1).  NaN compares false both ways and changes nothing.
   __device__ __forceinline__ void add(O x, int64_t jj) {
     const bool b = better(x, v);
-    const bool e = (x == v);
-    const bool take = b || (e && c == 0);
-    j = take ? jj : j;
-    c = b ? 1 : c + (e ? 1 : 0);
+    const bool ge = better_eq(x, v);
+    const int32_t cn = b ? 1 : c + (ge ? 1 : 0);
+    j = (ge && cn == 1) ? jj : j;
+    c = cn;
     v = b ? x : v;
   }
   __device__ __forceinline__ void merge(const SelAcc &o) {
@@ -127,11 +142,11 @@ template <class O, bool IS_MAX> struct SelAcc {
   }
 };
 
-// Accumulators used inside a column walk (reduce_col_kernel).  Sums use
-// SumAcc itself.  Max/min keep the index as a 32-bit offset from the
-// segment's first row -- the row is wave-uniform there, so the fold selects
-// one 32-bit register instead of a 64-bit pair -- and widen it once at the
-// end.  The update rule is SelAcc::add's.
+// Accumulators used inside a segment walk (reduce_col_kernel, and
+// reduce_row_kernel when the segment is shorter than 2^31).  Sums use SumAcc
+// itself.  Max/min keep the index as a 32-bit offset from the segment's
+// first element -- one 32-bit select per element instead of a 64-bit pair --
+// and widen it once at the end.  The update rule is SelAcc::add's.
 template <class O, bool IS_MAX> struct SelAcc32 {
   O v;
   int32_t j;
@@ -142,15 +157,22 @@ template <class O, bool IS_MAX> struct SelAcc32 {
     j = 0;
     c = 0;
   }
+  // SelAcc::add's rule: two compares, an add-with-carry and three selects
+  // per element (the 64-bit form with a separate equality test took about
+  // twice as many instructions).
   __device__ __forceinline__ void add(O x, int32_t jj) {
     const bool b = SelAcc<O, IS_MAX>::better(x, v);
-    const bool e = (x == v);
-    const bool take = b || (e && c == 0);
-    j = take ? jj : j;
-    c = b ? 1 : c + (e ? 1 : 0);
+    const bool ge = SelAcc<O, IS_MAX>::better_eq(x, v);
+    const int32_t cn = b ? 1 : c + (ge ? 1 : 0);
+    j = (ge && cn == 1) ? jj : j;
+    c = cn;
     v = b ? x : v;
   }
 };
+
+template <class Acc> struct IsSel : std::false_type {};
+template <class O, bool IS_MAX>
+struct IsSel<SelAcc<O, IS_MAX>> : std::true_type {};
 
 template <class Acc> struct ColLocal {
   using type = Acc;
@@ -238,7 +260,7 @@ struct DropDesc {
 
 // Slices are contiguous runs of length D starting at x + keep.offset_of(k).
 // Block b handles slice k = b / S, segment s = b % S: j in [s*seg, ..).
-template <class T, class O, class Acc, int VEC, int MODE>
+template <class T, class O, class Acc, int VEC, int MODE, bool IDX32>
 __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
     const T *__restrict__ x, KeepDesc keep, int64_t D, int64_t seg, int S,
     Acc *partial, RedOut<MODE> out) {
@@ -248,8 +270,20 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
   const T *row = x + keep.offset_of(k);
   const int64_t j0 = int64_t(s) * seg;
   const int64_t j1 = j0 + seg < D ? j0 + seg : D;
-  Acc a;
-  a.init();
+  // IDX32 (seg < 2^31): max/min accumulate a 32-bit index relative to j0
+  // and widen it once at the end.
+  using LA = std::conditional_t<IDX32, typename ColLocal<Acc>::type, Acc>;
+  using IT = std::conditional_t<IDX32, int32_t, int64_t>;
+  // Max/min: one accumulator per vector lane (element i of every vector
+  // goes to a[i]), so the per-element select chains are independent; each
+  // still sees its elements in increasing j, and the merge below keeps the
+  // smallest index on ties, so the result is the single-chain one.  Sums
+  // keep one chain (their rounding is order-dependent).
+  constexpr int NA = IsSel<Acc>::value ? VEC : 1;
+  LA a[NA];
+#pragma unroll
+  for (int q = 0; q < NA; ++q)
+    a[q].init();
   using V = VecT<T, VEC>;
   // NT_ROW_UR independent vector loads in flight per work-item, then the
   // tail.
@@ -261,24 +295,38 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
 #pragma unroll
     for (int u = 0; u < UR; ++u)
       v[u] = vload<true, T, VEC>(row + j + u * step);
+    const IT jb = IDX32 ? IT(j - j0) : IT(j);
 #pragma unroll
     for (int u = 0; u < UR; ++u)
 #pragma unroll
       for (int i = 0; i < VEC; ++i)
-        a.add(static_cast<O>(v[u].v[i]), j + u * step + i);
+        a[i % NA].add(static_cast<O>(v[u].v[i]), jb + IT(u * step + i));
   }
   for (; j < j1; j += step) {
+    const IT jb = IDX32 ? IT(j - j0) : IT(j);
     if (VEC > 1 && j + VEC <= j1) {
       const V v = vload<true, T, VEC>(row + j);
 #pragma unroll
       for (int i = 0; i < VEC; ++i)
-        a.add(static_cast<O>(v.v[i]), j + i);
+        a[i % NA].add(static_cast<O>(v.v[i]), jb + IT(i));
     } else {
       for (int i = 0; i < VEC && j + i < j1; ++i)
-        a.add(static_cast<O>(row[j + i]), j + i);
+        a[i % NA].add(static_cast<O>(row[j + i]), jb + IT(i));
     }
   }
-  Acc r = block_reduce(a, lds);
+  Acc aw;
+  if constexpr (IDX32)
+    aw = ColLocal<Acc>::widen(a[0], j0);
+  else
+    aw = a[0];
+#pragma unroll
+  for (int q = 1; q < NA; ++q) {
+    if constexpr (IDX32)
+      aw.merge(ColLocal<Acc>::widen(a[q], j0));
+    else
+      aw.merge(a[q]);
+  }
+  Acc r = block_reduce(aw, lds);
   if (threadIdx.x == 0) {
     if (S == 1)
       out.template write<O>(k, r);
@@ -318,6 +366,54 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
   using V = VecT<T, VEC>;
   if (k0 + VEC <= K) {
     int32_t jr = wr;
+#if NT_COL_PIPE
+    // Groups of UR rows (g-th group: rows wr + g*UR*WR + u*WR).  Max/min
+    // spend long enough on a group's selects that a wave would otherwise
+    // leave the memory pipe idle meanwhile: the next group's loads go out
+    // before this group's arithmetic, alternating two register sets (a copy
+    // between them would wait for the loads in flight).  The last prefetch
+    // re-reads the last group (clamped index, in bounds) and is discarded.
+    constexpr int32_t GR = UR * WR;
+    // wave-uniform loop control and addresses (scalar registers)
+    const int32_t wru = __builtin_amdgcn_readfirstlane(wr);
+    const int32_t nru = __builtin_amdgcn_readfirstlane(nr);
+    const int32_t ng = nru - 1 - wru - (UR - 1) * WR >= 0
+                           ? (nru - 1 - wru - (UR - 1) * WR) / GR + 1
+                           : 0;
+    if (IsSel<Acc>::value && ng > 0) {
+      V va[UR], vb[UR];
+      const int64_t rs = int64_t(WR) * sd, gs = int64_t(GR) * sd;
+      const T *pa = base + int64_t(wru) * sd; // group 0
+      auto load = [&](V *v, const T *p) {
+#pragma unroll
+        for (int u = 0; u < UR; ++u)
+          v[u] = vload<true, T, VEC>(p + u * rs);
+      };
+      auto fold = [&](const V *v, int32_t g) {
+        const int32_t jg = wru + g * GR;
+#pragma unroll
+        for (int u = 0; u < UR; ++u)
+#pragma unroll
+          for (int i = 0; i < VEC; ++i)
+            la[i].add(static_cast<O>(v[u].v[i]), jg + u * WR);
+      };
+      auto at = [&](int32_t g) { return pa + int64_t(g < ng ? g : ng - 1) * gs; };
+      load(va, pa);
+      int32_t g = 0;
+      for (; g + 1 < ng; g += 2) {
+        load(vb, at(g + 1));
+        // keep the scheduler from sinking these loads below the selects
+        __builtin_amdgcn_sched_barrier(0);
+        fold(va, g);
+        load(va, at(g + 2)); // the last group again when g + 2 == ng
+        __builtin_amdgcn_sched_barrier(0);
+        fold(vb, g + 1);
+      }
+      if (g < ng)
+        fold(va, g);
+      jr = wru + ng * GR;
+    }
+#endif
     for (; jr + (UR - 1) * WR < nr; jr += UR * WR) {
       V v[UR];
 #pragma unroll
@@ -622,14 +718,20 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out,
     const int64_t blocks = p.K * S;
     if (blocks >= (int64_t(1) << 31))
       fail(NT_ERR_RUNTIME, "reduction too large");
-    if (aligned)
-      reduce_row_kernel<T, O, Acc, VEC, MODE>
-          <<<dim3(unsigned(blocks)), RED_THREADS, 0, st>>>(
-              xp, kd, p.D, seg, int(S), partial, out);
+    const bool idx32 = seg < (int64_t(1) << 31);
+    const dim3 grid{unsigned(blocks), 1u, 1u};
+    if (aligned && idx32)
+      reduce_row_kernel<T, O, Acc, VEC, MODE, true>
+          <<<grid, RED_THREADS, 0, st>>>(xp, kd, p.D, seg, int(S), partial, out);
+    else if (aligned)
+      reduce_row_kernel<T, O, Acc, VEC, MODE, false>
+          <<<grid, RED_THREADS, 0, st>>>(xp, kd, p.D, seg, int(S), partial, out);
+    else if (idx32)
+      reduce_row_kernel<T, O, Acc, 1, MODE, true>
+          <<<grid, RED_THREADS, 0, st>>>(xp, kd, p.D, seg, int(S), partial, out);
     else
-      reduce_row_kernel<T, O, Acc, 1, MODE>
-          <<<dim3(unsigned(blocks)), RED_THREADS, 0, st>>>(
-              xp, kd, p.D, seg, int(S), partial, out);
+      reduce_row_kernel<T, O, Acc, 1, MODE, false>
+          <<<grid, RED_THREADS, 0, st>>>(xp, kd, p.D, seg, int(S), partial, out);
     NT_LAUNCH_CHECK();
     finish(partial, int(S));
     return;
