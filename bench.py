@@ -812,6 +812,10 @@ def cpu_parts() -> dict:
 
 # ---------------------------------------------------------------- profiles
 
+PMC_SET1 = ("SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_WAIT_INST_LDS "
+            "SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS GRBM_GUI_ACTIVE")
+PMC_SET2 = ("SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_INSTS_LDS SQ_INSTS_VMEM_RD SQ_INSTS_VMEM_WR "
+            "SQ_INST_LEVEL_VMEM SQ_ACTIVE_INST_VMEM SQ_LEVEL_WAVES GRBM_GUI_ACTIVE")
 _PROF = "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/{d} -o run -- python -u bench.py {a}"
 _PMC = "rocprofv3 --pmc {c} --output-format csv -d gpurun_out/{d} -o run -- python -u bench.py {a}"
 PROFILE_CMDS = {
@@ -826,6 +830,16 @@ PROFILE_CMDS = {
         d="prof_mm_pmc", a="--parts mm"),
     "fetch": _PMC.format(c="FETCH_SIZE", d="prof_fetch", a="--steps 1 --warmup 0 --parts ew --calib"),
     "write": _PMC.format(c="WRITE_SIZE", d="prof_write", a="--steps 1 --warmup 0 --parts ew --calib"),
+    # issue / wait / occupancy counters, two passes per part
+    "ew_pmc1": _PMC.format(c=PMC_SET1, d="prof_ew_pmc1", a="--steps 1 --warmup 0 --parts ew"),
+    "ew_pmc2": _PMC.format(c=PMC_SET2, d="prof_ew_pmc2", a="--steps 1 --warmup 0 --parts ew"),
+    "red_pmc1": _PMC.format(c=PMC_SET1, d="prof_red_pmc1", a="--parts red"),
+    "red_pmc2": _PMC.format(c=PMC_SET2, d="prof_red_pmc2", a="--parts red"),
+    # HBM bytes of the reductions and of the MLP step (same calibration)
+    "red_fetch": _PMC.format(c="FETCH_SIZE", d="prof_red_fetch", a="--parts red --calib"),
+    "red_write": _PMC.format(c="WRITE_SIZE", d="prof_red_write", a="--parts red --calib"),
+    "mlp_fetch": _PMC.format(c="FETCH_SIZE", d="prof_mlp_fetch", a="--parts mlp --mlp-steps 3 --calib"),
+    "mlp_write": _PMC.format(c="WRITE_SIZE", d="prof_mlp_write", a="--parts mlp --mlp-steps 3 --calib"),
 }
 PROFILE_FILES = {
     "sweep": ("elementwise_sweep_config2_trace.md", "Kernel statistics: config-2 elementwise sweep (the headline)"),
@@ -903,9 +917,135 @@ def _summarize_mm_pmc(path: str, out_md: str) -> None:
                     f"{util:.3f} | {lw:.3f} | {bc:.0f} |\n")
 
 
+def _load_pmc(path: str) -> dict:
+    """{(kernel, grid): {counter or "dur_ns": per-dispatch average}}."""
+    import csv
+    acc: dict[tuple, dict] = {}
+    for r in csv.DictReader(open(os.path.join(path, "run_counter_collection.csv"))):
+        key = (_short(r["Kernel_Name"]), int(r["Grid_Size"]))
+        d = acc.setdefault(key, {})
+        disp = d.setdefault(r["Dispatch_Id"], {
+            "dur_ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+        disp[r["Counter_Name"]] = float(r["Counter_Value"])
+    out = {}
+    for key, d in acc.items():
+        ds = list(d.values())
+        names = set().union(*[x.keys() for x in ds])
+        out[key] = {n: sum(x.get(n, 0.0) for x in ds) / len(ds) for n in names}
+        out[key]["dispatches"] = len(ds)
+    return out
+
+
+def _summarize_pmc(part: str, dirs: list[str], out_md: str, title: str, keep) -> None:
+    """Issue, wait, occupancy and LDS figures per kernel from the two counter
+    passes (PMC_SET1, PMC_SET2) of one bench part."""
+    cus, simds, clk = 256, 1024, 2.4
+    a, b = _load_pmc(dirs[0]), _load_pmc(dirs[1])
+    rows = []
+    for key in sorted(a):
+        name, grid = key
+        if not keep(name):
+            continue
+        x, y = a[key], b.get(key, {})
+        cyc = x["dur_ns"] * clk
+        wc = max(x.get("SQ_WAVE_CYCLES", 0.0), 1.0)
+        rows.append((name, grid, int(x["dispatches"]), x["dur_ns"] / 1e3,
+                     wc * 4 / (cus * cyc),                       # resident waves per CU
+                     x.get("SQ_WAIT_ANY", 0.0) / wc,              # waiting (s_waitcnt, barrier)
+                     x.get("SQ_WAIT_INST_ANY", 0.0) / wc,         # ready, not issued
+                     x.get("SQ_WAIT_INST_LDS", 0.0) / wc,
+                     y.get("SQ_ACTIVE_INST_VALU", 0.0) * 4 / (simds * cyc) if y else float("nan"),
+                     y.get("SQ_INSTS_VALU", 0.0) / max(x.get("SQ_WAVES", 1.0), 1.0) if y else float("nan"),
+                     x.get("SQ_LDS_BANK_CONFLICT", 0.0) / (cus * cyc),
+                     y.get("SQ_INST_LEVEL_VMEM", 0.0) / max(
+                         y.get("SQ_INSTS_VMEM_RD", 0.0) + y.get("SQ_INSTS_VMEM_WR", 0.0), 1.0)
+                     if y else float("nan")))
+    with open(out_md, "w") as o:
+        o.write(f"# {title}\n\nCommands (repo root on the GPU box):\n\n```\n"
+                f"{PROFILE_CMDS[part + '_pmc1']}\n{PROFILE_CMDS[part + '_pmc2']}\n```\n\n"
+                f"Summarised with `python bench.py --summarize {part}_pmc gpurun_out/prof_{part}_pmc1 "
+                f"gpurun_out/prof_{part}_pmc2`.  Per dispatch, averaged; durations from the first "
+                "(counter-collecting) pass.  SQ cycle counters are summed over the GPU's waves in "
+                "units of 4 cycles (so resident waves per CU = 4 x SQ_WAVE_CYCLES / (256 CUs x "
+                "cycles), at most 32):\n\n"
+                "* waves/CU: average resident waves per CU;\n"
+                "* wait: share of wave time in s_waitcnt / barrier waits (SQ_WAIT_ANY / SQ_WAVE_CYCLES);\n"
+                "* issue-wait: share of wave time ready but not issued (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES);\n"
+                "* LDS-wait: SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES;\n"
+                "* VALU busy: SIMD cycles issuing VALU / (1024 SIMDs x cycles);\n"
+                "* VALU/wave: VALU instructions per wave;\n"
+                "* bank-conflict: LDS bank-conflict cycles per CU / cycles;\n"
+                "* VMEM level/inst: SQ_INST_LEVEL_VMEM / VMEM instructions (a latency proxy, "
+                "cycles x 4).\n\n"
+                "| kernel | grid | dispatches | us | waves/CU | wait | issue-wait | LDS-wait | "
+                "VALU busy | VALU/wave | bank-conflict | VMEM level/inst |\n"
+                "|---|---|---|---|---|---|---|---|---|---|---|---|\n")
+        for r in rows:
+            o.write(f"| `{r[0][:110]}` | {r[1]} | {r[2]} | {r[3]:.1f} | {r[4]:.1f} | {r[5]:.2f} | "
+                    f"{r[6]:.2f} | {r[7]:.3f} | {r[8]:.2f} | {r[9]:.0f} | {r[10]:.3f} | {r[11]:.0f} |\n")
+
+
+def _summarize_bytes(part: str, dirs: list[str], out_md: str, title: str, expect) -> None:
+    """HBM bytes per dispatch of every kernel of one part from the
+    FETCH_SIZE / WRITE_SIZE passes, scaled by the 2^24 copy of --calib."""
+    f, w = _load_pmc(dirs[0]), _load_pmc(dirs[1])
+    copy = [k for k in f if "CastOp<float, float>" in k[0] and k[1] == N_ELEM // 4]
+    fs = 64 * 1024 / f[copy[0]]["FETCH_SIZE"]
+    ws = 64 * 1024 / w[copy[0]]["WRITE_SIZE"]
+    with open(out_md, "w") as o:
+        o.write(f"# {title}\n\nCommands (repo root on the GPU box):\n\n```\n"
+                f"{PROFILE_CMDS[part + '_fetch']}\n{PROFILE_CMDS[part + '_write']}\n```\n\n"
+                f"Summarised with `python bench.py --summarize {part}_bytes gpurun_out/prof_{part}_fetch "
+                f"gpurun_out/prof_{part}_write`.  Calibration: the 2^24-element copy of --calib "
+                f"(64 MiB read, 64 MiB written) reads FETCH_SIZE {f[copy[0]]['FETCH_SIZE'] / 1024:.1f} MiB "
+                f"and WRITE_SIZE {w[copy[0]]['WRITE_SIZE'] / 1024:.1f} MiB, so FETCH_SIZE is scaled by "
+                f"{fs:.3f} and WRITE_SIZE by {ws:.3f}; `expected` is the algorithmic count "
+                "(each operand read once, each output written once) where the kernel's role is "
+                "known.\n\n"
+                "| kernel | grid | dispatches | read MiB | written MiB | expected read / written MiB |\n"
+                "|---|---|---|---|---|---|\n")
+        for key in sorted(f):
+            if key in copy or key[0].startswith("_rocclr") or key[0].startswith("__amd"):
+                continue
+            rd = f[key]["FETCH_SIZE"] * fs / 1024
+            wr_ = w.get(key, {}).get("WRITE_SIZE", 0.0) * ws / 1024
+            if rd + wr_ < 1.0:
+                continue
+            o.write(f"| `{key[0][:110]}` | {key[1]} | {int(f[key]['dispatches'])} | {rd:.1f} | "
+                    f"{wr_:.1f} | {expect(key[0], key[1]) or ''} |\n")
+
+
+def _red_expect(name: str, grid: int) -> str:
+    if name.startswith(("reduce_row_kernel", "reduce_col_kernel")):
+        return "256 / partials"
+    if name.startswith(("sel_bwd", "ew_rows_kernel<float, float, 1", "ew_flat_kernel<float, float, 1")):
+        return "0 (g, index, count: 0.1) / 256"
+    if name.startswith(("ew_rows_kernel<float, float, 2", "ew_flat_kernel<float, float, 2")):
+        return "256 / 256"
+    return ""
+
+
 def summarize(kind: str, dirs: list[str]) -> None:
     import csv
     prof = os.path.join(ROOT, "profiles")
+    if kind == "ew_pmc":
+        _summarize_pmc("ew", dirs, os.path.join(prof, "elementwise_sweep_config2_counters.md"),
+                       "Issue and wait counters: config-2 elementwise sweep kernels",
+                       lambda n: n.startswith(("ew_flat_kernel", "ew_tile4_kernel")))
+        return
+    if kind == "red_pmc":
+        _summarize_pmc("red", dirs, os.path.join(prof, "reduce_config3_counters.md"),
+                       "Issue and wait counters: config-3 reduction kernels",
+                       lambda n: not n.startswith(("_rocclr", "__amd")))
+        return
+    if kind == "red_bytes":
+        _summarize_bytes("red", dirs, os.path.join(prof, "reduce_config3_hbm_traffic.md"),
+                         "HBM traffic per launch: config-3 reductions", _red_expect)
+        return
+    if kind == "mlp_bytes":
+        _summarize_bytes("mlp", dirs, os.path.join(prof, "mlp_config5_hbm_traffic.md"),
+                         "HBM traffic per launch: config-5 MLP step kernels", lambda n, g: "")
+        return
     if kind in PROFILE_FILES:
         fname, title = PROFILE_FILES[kind]
         rows = list(csv.DictReader(open(os.path.join(dirs[0], "run_kernel_stats.csv"))))
@@ -990,7 +1130,8 @@ def main() -> int:
                          "written each): the reference dispatch for HBM byte counters")
     ap.add_argument("--summarize", nargs="+", metavar=("KIND", "DIR"),
                     help="write a profiles/ summary from rocprofv3 csv output: "
-                         "sweep|red|mm|mlp|next|mm_pmc DIR, or traffic FETCH_DIR WRITE_DIR")
+                         "sweep|red|mm|mlp|next|mm_pmc DIR, traffic|red_bytes|mlp_bytes "
+                         "FETCH_DIR WRITE_DIR, or ew_pmc|red_pmc PMC1_DIR PMC2_DIR")
     args = ap.parse_args()
     if args.summarize:
         summarize(args.summarize[0], args.summarize[1:])
