@@ -833,6 +833,8 @@ PROFILE_CMDS = {
     # issue / wait / occupancy counters, two passes per part
     "ew_pmc1": _PMC.format(c=PMC_SET1, d="prof_ew_pmc1", a="--steps 1 --warmup 0 --parts ew"),
     "ew_pmc2": _PMC.format(c=PMC_SET2, d="prof_ew_pmc2", a="--steps 1 --warmup 0 --parts ew"),
+    "mm_pmc1": _PMC.format(c=PMC_SET1, d="prof_mm_pmc1", a="--parts mm"),
+    "mm_pmc2": _PMC.format(c=PMC_SET2, d="prof_mm_pmc2", a="--parts mm"),
     "red_pmc1": _PMC.format(c=PMC_SET1, d="prof_red_pmc1", a="--parts red"),
     "red_pmc2": _PMC.format(c=PMC_SET2, d="prof_red_pmc2", a="--parts red"),
     # HBM bytes of the reductions and of the MLP step (same calibration)
@@ -1037,6 +1039,11 @@ def summarize(kind: str, dirs: list[str]) -> None:
         _summarize_pmc("red", dirs, os.path.join(prof, "reduce_config3_counters.md"),
                        "Issue and wait counters: config-3 reduction kernels",
                        lambda n: not n.startswith(("_rocclr", "__amd")))
+        return
+    if kind == "mm_pmc12":
+        _summarize_pmc("mm", dirs, os.path.join(prof, "matmul_config4_counters.md"),
+                       "Issue and wait counters: config-4 matmul kernels",
+                       lambda n: n.startswith("mm_"))
         return
     if kind == "red_bytes":
         _summarize_bytes("red", dirs, os.path.join(prof, "reduce_config3_hbm_traffic.md"),

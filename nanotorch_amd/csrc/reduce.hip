@@ -60,6 +60,9 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 // Max/min column walks issue the next UR rows' loads before the current
 // rows' selects (measured on [8192, 8192] axis 0: 0.60 -> 0.675 of peak at one
 // workgroup per CU; without it two workgroups per CU were best).
+#ifndef NT_COMBINE_WIDE
+#define NT_COMBINE_WIDE 256 // work-items per slice when at most 64 slices (1024: same or slower)
+#endif
 #ifndef NT_COL_PIPE
 #define NT_COL_PIPE 1
 #endif
@@ -680,8 +683,8 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out,
   auto finish = [&](Acc *partial, int S) {
     if (S > 1) {
       if (p.K <= 64)
-        reduce_combine_kernel<O, Acc, MODE, 1024>
-            <<<dim3(unsigned(p.K)), 1024, 0, st>>>(partial, S, out);
+        reduce_combine_kernel<O, Acc, MODE, NT_COMBINE_WIDE>
+            <<<dim3(unsigned(p.K)), NT_COMBINE_WIDE, 0, st>>>(partial, S, out);
       else
         reduce_combine_kernel<O, Acc, MODE, RED_THREADS>
             <<<dim3(unsigned(p.K)), RED_THREADS, 0, st>>>(partial, S, out);
@@ -931,48 +934,69 @@ __global__ __launch_bounds__(256) void sel_bwd_2d_kernel(
   const int64_t c = (int64_t(blockIdx.x) * 64 + lane) * 4;
   const int64_t r0 = int64_t(blockIdx.y) * rpb;
   const int64_t r1 = r0 + rpb < Rr ? r0 + rpb : Rr;
-  if (c >= Cc)
-    return;
-  T gk[4];
-  int64_t ik[4];
-  bool ok[4];
+  const bool live = c < Cc;
+  auto put = [&](int64_t r, const T (&t)[4]) {
+    T *p = gx + r * Cc + c;
+    VecT<T, 4> o;
+    if constexpr (ACC) {
+      const VecT<T, 4> old = vload<true, T, 4>(p);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o.v[e] = old.v[e] + t[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o.v[e] = t[e];
+    }
+    *reinterpret_cast<VecT<T, 4> *>(p) = o;
+  };
   if constexpr (MODE == 1) {
+    // reduced axis leading: column c's g / idx / count, loaded once
+    if (!live)
+      return;
+    T gk[4];
+    int64_t ik[4];
+    bool ok[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       gk[e] = g[c + e];
       ik[e] = idx[c + e];
       ok[e] = cnt[c + e] == 1;
     }
-  }
-  for (int64_t r = r0 + w; r < r1; r += RED_WAVES) {
-    T *p = gx + r * Cc + c;
-    VecT<T, 4> o;
-    VecT<T, 4> old;
-    if constexpr (ACC)
-      old = vload<true, T, 4>(p);
-    if constexpr (MODE == 0) {
-      const T gr = g[r];
-      const int64_t ir = idx[r];
-      const bool okr = cnt[r] == 1;
+    for (int64_t r = r0 + w; r < r1; r += RED_WAVES) {
+      T t[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const T t = gr * ((okr && c + e == ir) ? T(1) : T(0));
-        if constexpr (ACC)
-          o.v[e] = old.v[e] + t;
-        else
-          o.v[e] = t;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const T t = gk[e] * ((ok[e] && r == ik[e]) ? T(1) : T(0));
-        if constexpr (ACC)
-          o.v[e] = old.v[e] + t;
-        else
-          o.v[e] = t;
-      }
+      for (int e = 0; e < 4; ++e)
+        t[e] = gk[e] * ((ok[e] && r == ik[e]) ? T(1) : T(0));
+      put(r, t);
     }
-    *reinterpret_cast<VecT<T, 4> *>(p) = o;
+  } else {
+    // reduced axis trailing: row r's g / idx / count.  The block stages
+    // its rows' values in LDS (one coalesced load per chunk of 256 rows)
+    // so that the store stream does not wait on a load per row.
+    __shared__ T sg[256];
+    __shared__ int64_t si[256];
+    for (int64_t rc = r0; rc < r1; rc += 256) {
+      const int64_t nrc = r1 - rc < 256 ? r1 - rc : 256;
+      if (threadIdx.x < nrc) {
+        const int64_t r = rc + threadIdx.x;
+        sg[threadIdx.x] = g[r];
+        // a tie (count != 1) routes nothing: no column matches -1
+        si[threadIdx.x] = cnt[r] == 1 ? idx[r] : int64_t(-1);
+      }
+      __syncthreads();
+      if (live)
+        for (int q = w; q < nrc; q += RED_WAVES) {
+          const T gr = sg[q];
+          const int64_t ir = si[q];
+          T t[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            t[e] = gr * ((c + e == ir) ? T(1) : T(0));
+          put(rc + q, t);
+        }
+      __syncthreads();
+    }
   }
 }
 
