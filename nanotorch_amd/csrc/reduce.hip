@@ -66,6 +66,9 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 #ifndef NT_COL_PIPE
 #define NT_COL_PIPE 1
 #endif
+#ifndef NT_COL_UR_SEL
+#define NT_COL_UR_SEL 4 // pipelined max/min walk: 0.70 of peak at 4 rows a group, 0.65-0.68 at 6, 0.66-0.68 at 3, 0.69 at 5
+#endif
 #ifndef NT_COL_WG_SEL
 #define NT_COL_WG_SEL 1 // measured with NT_COL_PIPE: 0.675 / 0.51 of peak at 1 / 2
 #endif
@@ -749,7 +752,7 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out,
     const int vec = aligned ? VEC : 1;
     // Wide tensors: WC waves side by side (64 * vec * WC columns per
     // workgroup); narrow ones: 1 column group, 4 wave rows.
-    constexpr int UR = NT_COL_UR;
+    constexpr int UR = IsSel<Acc>::value ? NT_COL_UR_SEL : NT_COL_UR;
     constexpr int WC = NT_COL_WC;
     const int wc = K >= WC * 64 * vec ? WC : 1;
     const int64_t bx = ceil_div(K, int64_t(64) * vec * wc);
