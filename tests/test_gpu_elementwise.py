@@ -436,3 +436,30 @@ def test_pow_backward_exponent_classes(gpu, e):
     got = host(nt.Tensor._new_contiguous(K.unary_bwd(_lib.POW, dev(g), dev(a), e, None),
                                          a.shape))
     _assert_pow_close(got, want, 1e-6, f"pow bwd e={e}")
+
+
+@pytest.mark.parametrize("R", [1, 2, 3, 7, 8, 255, 256])
+@pytest.mark.parametrize("C", [4, 1024, 4100])
+def test_broadcast_rows_kernel(gpu, R, C):
+    """Contiguous [R, C] results with a broadcast row (bias: strides (0, 1)),
+    a broadcast column (strides (s, 0)) and a scalar, even and odd row
+    counts (the row-broadcast kernel takes two rows per work-item when R
+    is even), forward and accumulate, against the oracle, bit-exact."""
+    r = rng(seed_of("rows", R, C))
+    a = r.standard_normal((R, C)).astype(np.float32)
+    row = r.standard_normal(C).astype(np.float32)
+    col = r.standard_normal(R).astype(np.float32)
+    xa = dev(a)
+    got = host(xa + dev(row))
+    assert_bitexact(got, O.binary(O.ADD, a, np.broadcast_to(row, (R, C))), "bias")
+    got = host(xa * dev(col.reshape(R, 1)).expand(R, C))
+    assert_bitexact(got, O.binary(O.MUL, a, np.broadcast_to(col.reshape(R, 1), (R, C))), "column")
+    old = r.standard_normal((R, C)).astype(np.float32)
+    tgt = dev(old)
+    K.inplace(_lib.ADD, tgt, dev(row).reshape(1, C).expand(R, C))
+    assert_bitexact(host(tgt), O.accumulate(old, np.ascontiguousarray(np.broadcast_to(row, (R, C)))),
+                    "accumulate row")
+    tgt = dev(old)
+    K.inplace(_lib.ADD, tgt, dev(col).reshape(R, 1).expand(R, C))
+    assert_bitexact(host(tgt), O.accumulate(old, np.ascontiguousarray(np.broadcast_to(col.reshape(R, 1), (R, C)))),
+                    "accumulate column")

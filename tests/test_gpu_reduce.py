@@ -227,3 +227,24 @@ def test_config3_full_size(gpu, axes):
     K.reduce_bwd(_lib.R_MEAN, dev(g), float(n), None, None, axes, shape, tgt)
     want = O.binary(O.DIV, gb, np.broadcast_to(O.scalar(n, np.float32), shape))
     assert_bitexact(host(tgt), O.accumulate(old, want), "mean bwd acc 2^26")
+
+
+@pytest.mark.parametrize("D", [1, 2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 31, 33, 64, 100, 257])
+@pytest.mark.parametrize("K_", [2048, 1028])
+def test_column_walk_row_counts(gpu, D, K_):
+    """Max / min / sum along axis 0 of [D, K] for every small row count: the
+    column walk's pipelined groups of rows (none, one, an odd or even
+    number, a tail), its segment split and the wide (K >= 1024) and
+    unaligned-width (K % 1024 != 0) column blocks; values, first indices
+    and tie counts bit-exact (small integers: many ties)."""
+    r = rng(seed_of("colwalk", D, K_))
+    a = r.integers(-3, 4, (D, K_)).astype(np.float32)
+    x = dev(a)
+    for op, oop, aop in ((_lib.R_MAX, O.R_MAX, O.R_ARGMAX), (_lib.R_MIN, O.R_MIN, O.R_ARGMIN)):
+        v, idx, cnt = K.reduce(op, x, (0,), nt.float32, want_aux=True)
+        assert_bitexact(host(nt.Tensor._new_contiguous(v, (K_,))), O.reduce(oop, a, (0,)), f"{op} D={D}")
+        assert_bitexact(host(nt.Tensor._new_contiguous(idx, (K_,))), O.reduce(aop, a, (0,)), f"arg {op} D={D}")
+        want_cnt = (a == O.reduce(oop, a, (0,))[None, :]).sum(axis=0).astype(np.int32)
+        assert_bitexact(host(nt.Tensor._new_contiguous(cnt, (K_,))), want_cnt, f"count {op} D={D}")
+    got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, (0,), nt.float32), (K_,)))
+    assert_bitexact(got, a.sum(axis=0).astype(np.float32), f"sum D={D}")  # small integers: exact
