@@ -47,3 +47,55 @@ def test_traffic_calibrates_on_the_small_copies(tmp_path, monkeypatch):
     # 5 operands read and 2 written, 64 MiB each: the algorithmic 28 B/element
     assert t["per_launch_bytes"] == {"mul|transposed|bwd": bench.ew_bytes("mul", "bwd")}
     assert bench.ew_bytes("mul", "bwd") == 7 * 64 * 1024 * 1024
+
+
+def _write_pmc(path, rows):
+    """rows: (dispatch, kernel, grid, counter, value, duration_ns)."""
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "run_counter_collection.csv"), "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Grid_Size", "Kernel_Name", "Counter_Name",
+                                          "Counter_Value", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        for d, name, grid, counter, value, dur in rows:
+            w.writerow({"Dispatch_Id": d, "Grid_Size": grid, "Kernel_Name": name,
+                        "Counter_Name": counter, "Counter_Value": value,
+                        "Start_Timestamp": 1000 * d, "End_Timestamp": 1000 * d + dur})
+
+
+RED = "void nt::reduce_row_kernel<float, float, nt::SumAcc<float>, 4, 0, true>(...)"
+
+
+def test_counter_summary_ratios(tmp_path, monkeypatch):
+    # one 10-us dispatch at 2.4 GHz: 24,000 cycles; 8 resident waves per CU
+    # over the whole kernel = 8 * 256 * 24000 / 4 quad-cycles of SQ_WAVE_CYCLES
+    cyc = 10_000 * 2.4
+    wc = 8 * 256 * cyc / 4
+    s1 = [(1, RED, 131072, "SQ_WAVE_CYCLES", wc, 10_000), (1, RED, 131072, "SQ_WAIT_ANY", 0.5 * wc, 10_000),
+          (1, RED, 131072, "SQ_WAIT_INST_ANY", 0.25 * wc, 10_000), (1, RED, 131072, "SQ_WAVES", 2048, 10_000)]
+    # VALU busy half the time on every SIMD
+    s2 = [(1, RED, 131072, "SQ_ACTIVE_INST_VALU", 0.5 * 1024 * cyc / 4, 10_000),
+          (1, RED, 131072, "SQ_INSTS_VALU", 2048 * 100, 10_000)]
+    _write_pmc(tmp_path / "p1", s1)
+    _write_pmc(tmp_path / "p2", s2)
+    (tmp_path / "profiles").mkdir()
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    bench.summarize("red_pmc", [str(tmp_path / "p1"), str(tmp_path / "p2")])
+    row = [l for l in open(tmp_path / "profiles" / "reduce_config3_counters.md") if l.startswith("| `reduce")][0]
+    cells = [c.strip() for c in row.split("|")]
+    # kernel, grid, dispatches, us, waves/CU, wait, issue-wait, LDS-wait, VALU busy, VALU/wave
+    assert cells[4:11] == ["10.0", "8.0", "0.50", "0.25", "0.000", "0.50", "100"]
+
+
+def test_byte_summary_scales_by_the_copy(tmp_path, monkeypatch):
+    mib = 1024.0
+    f = [(1, COPY, (1 << 24) // 4, "FETCH_SIZE", 32 * mib, 1000), (2, RED, 131072, "FETCH_SIZE", 128 * mib, 1000)]
+    w = [(1, COPY, (1 << 24) // 4, "WRITE_SIZE", 64 * mib, 1000), (2, RED, 131072, "WRITE_SIZE", 0.0, 1000)]
+    _write_pmc(tmp_path / "f", f)
+    _write_pmc(tmp_path / "w", w)
+    (tmp_path / "profiles").mkdir()
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    bench.summarize("red_bytes", [str(tmp_path / "f"), str(tmp_path / "w")])
+    rows = [l for l in open(tmp_path / "profiles" / "reduce_config3_hbm_traffic.md") if l.startswith("| `")]
+    assert len(rows) == 1  # the calibration copy itself is not listed
+    cells = [c.strip() for c in rows[0].split("|")]
+    assert cells[4:6] == ["256.0", "0.0"]  # a 256 MiB read-only reduction
