@@ -621,23 +621,43 @@ __global__ __launch_bounds__(WD_THREADS, 1) void mm_f32_mfma_wide_kernel(
 // C[m][n] (+)= part[0][m][n] + part[1][m][n] + ... in slice order (a fixed
 // order: the result does not depend on scheduling).  Four columns per
 // work-item; N is a multiple of 4.
+template <int S, bool VEC_C>
 __global__ __launch_bounds__(256) void mm_splitk_sum_kernel(
-    const float *__restrict__ part, int S, int64_t M, int64_t N, float *C,
-    int64_t sCm, int64_t sCn, int accumulate) {
-  const int64_t n4 = N / 4;
-  const int64_t total = M * n4;
-  for (int64_t q = int64_t(blockIdx.x) * 256 + threadIdx.x; q < total;
-       q += int64_t(gridDim.x) * 256) {
-    const int64_t m = q / n4, n = (q - m * n4) * 4;
-    float4 v = *reinterpret_cast<const float4 *>(part + m * N + n);
-    for (int s = 1; s < S; ++s) {
-      const float4 w =
-          *reinterpret_cast<const float4 *>(part + (int64_t(s) * M + m) * N + n);
-      v.x = v.x + w.x;
-      v.y = v.y + w.y;
-      v.z = v.z + w.z;
-      v.w = v.w + w.w;
+    const float *__restrict__ part, int64_t M, int64_t N, float *C,
+    int64_t sCm, int64_t sCn, int accumulate, FastDivU32 fdn4, uint32_t total) {
+  // one work-item per 4 columns of one row, in a one-shot grid; the S slice
+  // loads are independent (S is a template argument) and go out together
+  const uint32_t q = blockIdx.x * 256u + threadIdx.x;
+  if (q >= total)
+    return;
+  const uint32_t n4 = uint32_t(N / 4);
+  const uint32_t m32 = fdn4.div(q);
+  const int64_t m = m32, n = int64_t(q - m32 * n4) * 4;
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 w[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    w[s] = __builtin_nontemporal_load(
+        reinterpret_cast<const f4 *>(part + (int64_t(s) * M + m) * N + n));
+  float4 v = make_float4(w[0].x, w[0].y, w[0].z, w[0].w);
+#pragma unroll
+  for (int s = 1; s < S; ++s) {
+    v.x = v.x + w[s].x;
+    v.y = v.y + w[s].y;
+    v.z = v.z + w[s].z;
+    v.w = v.w + w[s].w;
+  }
+  if constexpr (VEC_C) {
+    float4 *dst = reinterpret_cast<float4 *>(C + m * sCm + n);
+    if (accumulate) {
+      const float4 old = *dst;
+      v.x = old.x + v.x;
+      v.y = old.y + v.y;
+      v.z = old.z + v.z;
+      v.w = old.w + v.w;
     }
+    *dst = v;
+  } else {
     const float o[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -731,10 +751,31 @@ template <int LA, int LB> void launch_mfma(const MMArgs &a, int64_t blocks) {
                  stream()>>>(w);
           NT_LAUNCH_CHECK();
           const int64_t items = a.M * (a.N / 4);
-          const unsigned grid = unsigned(
-              std::min<int64_t>((items + 255) / 256, cus * 16));
-          mm_splitk_sum_kernel<<<grid, 256, 0, stream()>>>(
-              w.part, S, a.M, a.N, a.C, a.sCm, a.sCn, a.accumulate);
+          if (items >= (int64_t(1) << 32))
+            fail(NT_ERR_RUNTIME, "matmul: split-K output too large");
+          const unsigned grid = unsigned((items + 255) / 256);
+          const bool vec_c =
+              a.sCn == 1 && a.sCm % 4 == 0 &&
+              reinterpret_cast<uintptr_t>(a.C) % 16 == 0;
+          const FastDivU32 fdn4{uint32_t(a.N / 4)};
+#define NT_SPLITK_SUM(SS)                                                      \
+  do {                                                                         \
+    if (vec_c)                                                                 \
+      mm_splitk_sum_kernel<SS, true><<<grid, 256, 0, stream()>>>(              \
+          w.part, a.M, a.N, a.C, a.sCm, a.sCn, a.accumulate, fdn4,             \
+          uint32_t(items));                                                    \
+    else                                                                       \
+      mm_splitk_sum_kernel<SS, false><<<grid, 256, 0, stream()>>>(             \
+          w.part, a.M, a.N, a.C, a.sCm, a.sCn, a.accumulate, fdn4,             \
+          uint32_t(items));                                                    \
+  } while (0)
+          if (S == 2)
+            NT_SPLITK_SUM(2);
+          else if (S == 4)
+            NT_SPLITK_SUM(4);
+          else
+            NT_SPLITK_SUM(8);
+#undef NT_SPLITK_SUM
           return;
         }
       }
