@@ -248,3 +248,40 @@ def test_column_walk_row_counts(gpu, D, K_):
         assert_bitexact(host(nt.Tensor._new_contiguous(cnt, (K_,))), want_cnt, f"count {op} D={D}")
     got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, (0,), nt.float32), (K_,)))
     assert_bitexact(got, a.sum(axis=0).astype(np.float32), f"sum D={D}")  # small integers: exact
+
+
+def test_split_slices_back_to_back(gpu):
+    """Reductions whose slices are split over several workgroups (row and
+    generic kernels), queued back to back with no host wait between them,
+    so each launch's partials reuse memory that earlier launches with other
+    slice and segment counts wrote.  Every result must be exact: small
+    integers make fp32 sums exact and give max/min many ties."""
+    r = rng(seed_of("split-slices"))
+    cases = [
+        ((1, 1 << 20), (1,)),       # row kernel, one slice in 256 segments
+        ((3, 300001), (1,)),        # row kernel, unaligned rows (scalar loads)
+        ((1 << 21,), (0,)),         # full reduction
+        ((17, 65536), (1,)),
+        ((255, 8192), (1,)),        # two segments per slice
+        ((64, 9, 4000), (0, 2)),    # generic kernel, 9 slices
+        ((1000, 3, 700), (0, 2)),   # generic kernel, 3 slices
+    ]
+    pending = []
+    for shape, axes in cases * 2:
+        a = r.integers(-3, 4, shape).astype(np.float32)
+        x = dev(a)
+        kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+        s = K.reduce(_lib.R_SUM, x, axes, nt.float32)
+        v, idx, cnt = K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True)
+        am = K.reduce(_lib.R_ARGMIN, x, axes, nt.int64)
+        pending.append((a, axes, kshape, s, v, idx, cnt, am, x))
+    for a, axes, kshape, s, v, idx, cnt, am, _ in pending:
+        tag = f"{a.shape} {axes}"
+        want_sum = a.astype(np.int64).sum(axis=axes).astype(np.float32)
+        assert_bitexact(host(nt.Tensor._new_contiguous(s, kshape)), want_sum, "sum " + tag)
+        want_max = O.reduce(O.R_MAX, a, axes)
+        assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), want_max, "max " + tag)
+        assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(O.R_ARGMAX, a, axes), "argmax " + tag)
+        want_cnt = (a == np.expand_dims(want_max, axes)).sum(axis=axes).astype(np.int32)
+        assert_bitexact(host(nt.Tensor._new_contiguous(cnt, kshape)), want_cnt, "count " + tag)
+        assert_bitexact(host(nt.Tensor._new_contiguous(am, kshape)), O.reduce(O.R_ARGMIN, a, axes), "argmin " + tag)
