@@ -8,11 +8,13 @@
 //               broadcast row, a broadcast column or a scalar: flat-kernel
 //               I/O with the (row, column) of each vector from one
 //               multiply-high division.
-//  * tile2d  -- after merging dims, the iteration space is 2-D.  A 64x64 tile
-//               per workgroup; operands whose rows are contiguous are read
-//               straight; operands contiguous along the other axis (e.g.
-//               `x.T`) are staged through a padded LDS tile so both the
-//               global read and the global write stay coalesced.  Outputs
+//  * tile2d  -- after merging dims, the iteration space is 2-D.  One tile
+//               per workgroup (64x64; fp32 also 128x64 and 64x128, chosen
+//               by the streams in each layout); operands whose rows are
+//               contiguous are read straight; operands contiguous along the
+//               other axis (e.g. `x.T`) are staged through a padded LDS tile
+//               so both the global read and the global write stay
+//               coalesced.  Outputs
 //               laid out that way go back through the same LDS tile.  The
 //               tile walks whichever orientation exchanges less.  With
 //               4-aligned sizes and strides every access is a 16-byte vector
@@ -287,19 +289,19 @@ __global__ __launch_bounds__(NT_ROWS_THREADS) void ew_rows_kernel(
 
 // --------------------------------------------------------------- tile2d x4
 
-// 64x64 tile with 4-element vector accesses (16 B for fp32).  Work-item t
-// owns, for i < 4, row rl = (t + 256 i) / 16 and the four columns
-// 4 * ((t + 256 i) % 16) + 0..3 of the tile.
-//  * ROW operands (unit column stride) are read/written straight in that
-//    layout: 16 work-items cover one 256-byte row segment.
-//  * COL operands (unit row stride, e.g. `x.T`) are read as 4 consecutive
-//    rows of one column -- again 256-byte segments -- and exchanged through a
-//    padded [col][row] LDS tile (row length 65: a wave's accesses hit
-//    distinct banks).  Outputs of that layout take the reverse path.
+// TR x TC tile (TR rows by TC columns of the iteration space) with 4-element
+// vector accesses (16 B for fp32), TR * TC / 16 work-items.
+//  * ROW operands (unit column stride) are read/written straight: TC / 4
+//    work-items cover one row segment of TC elements (256 bytes of fp32 at
+//    TC = 64).
+//  * COL operands (unit row stride, e.g. `x.T`) are read as column segments
+//    of TR elements, 4 consecutive rows per work-item, and exchanged through
+//    a [col][row] LDS tile whose rows are padded to TR + 1 elements (a
+//    wave's accesses spread over the banks).  Outputs of that layout take
+//    the reverse path.
 //  * Other operands (stride-0 broadcasts, general strides) are read per
-//    element in the owner layout.
-// All global loads of all inputs are issued before the first LDS exchange;
-// COL operands share two LDS buffers, two at a time.
+//    element in the owner (ROW) layout.
+// All global loads of all inputs are issued before the first LDS exchange.
 // Tile (tr, tc) of workgroup b in a tiles_r x tiles_c grid (fewer than 2^24
 // tiles), in diagonal order: consecutive workgroups take consecutive tile
 // columns, each one tile row further on, tr = (b / tiles_c + tc) mod tiles_r.
@@ -319,19 +321,25 @@ __device__ __forceinline__ void diagonal_tile(uint32_t b, int64_t tiles_r,
   tr = (q + c) % nr;
 }
 
-template <class TI, class TO, int NI, int NO, bool NTL, class F>
-__global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
+template <class TI, class TO, int NI, int NO, bool NTL, int TR, int TC,
+          class F>
+__global__ __launch_bounds__(TR *TC / 16) void ew_tile4_kernel(
     PtrPack<const TI, NI> in, Strides2<NI> sin, uint32_t row_in,
     uint32_t col_in, uint32_t bcol_in, PtrPack<TO, NO> out, Strides2<NO> sout,
     uint32_t row_out, uint32_t col_out, int64_t R, int64_t C, int64_t tiles_c,
     F f) {
-  constexpr int T = EW_TILE, P = EW_TILE_PAD, EL = 4;
+  // NTH work-items, each owning EL = 4 vectors of 4 elements per operand.
+  // ROW ownership: vector f = t + NTH * i is row l = f / QC, columns
+  // 4 * (f % QC) + 0..3; COL ownership: column f / QR, rows
+  // 4 * (f % QR) + 0..3.
+  constexpr int NTH = TR * TC / 16, EL = 4, PR = TR + 1;
+  constexpr int QC = TC / 4, QR = TR / 4;
   constexpr size_t LB = sizeof(TI) > sizeof(TO) ? sizeof(TI) : sizeof(TO);
-  __shared__ __align__(16) unsigned char lds_raw[EW_TILE_BUFS][T * P * LB];
+  __shared__ __align__(16) unsigned char lds_raw[EW_TILE_BUFS][TC * PR * LB];
   const int t = threadIdx.x;
   int64_t tr, tc;
-  diagonal_tile(blockIdx.x, (R + T - 1) / T, tiles_c, tr, tc);
-  const int64_t r0 = tr * T, c0 = tc * T;
+  diagonal_tile(blockIdx.x, (R + TR - 1) / TR, tiles_c, tr, tc);
+  const int64_t r0 = tr * TR, c0 = tc * TC;
 
   TI v[NI > 0 ? NI : 1][EL][4];
 #pragma unroll
@@ -340,10 +348,11 @@ __global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
     const int64_t sr = sin.r[k], sc = sin.c[k];
 #pragma unroll
     for (int i = 0; i < EL; ++i) {
-      const int f_ = t + EW_THREADS * i;
-      const int q = f_ & 15, l = f_ >> 4;
+      const unsigned f_ = unsigned(t + NTH * i);
+      const int q = int(f_ % QC), l = int(f_ / QC);
       if (col_in & (1u << k)) {
-        const int64_t r = r0 + 4 * q, c = c0 + l; // raw COL layout
+        const int qq = int(f_ % QR), ll = int(f_ / QR);
+        const int64_t r = r0 + 4 * qq, c = c0 + ll; // raw COL layout
         if (r < R && c < C) {
           const VecT<TI, 4> w = vload<NTL, TI, 4>(p + r + c * sc);
 #pragma unroll
@@ -374,13 +383,14 @@ __global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
       }
     }
   }
-  // LDS exchange of COL inputs: one round (and one barrier) per operand.
-  // With two buffers the rounds alternate between them: a buffer is
-  // rewritten two rounds after it was read, and every work-item has passed
-  // the barrier of the round in between, so its reads are complete.  With
-  // one buffer each round after the first waits at a barrier of its own
-  // before it writes.  The number of rounds follows the layout masks, which
-  // are kernel arguments, so every such barrier is workgroup-uniform.
+  // LDS exchange of COL inputs ([column][row] tile, rows padded to TR + 1):
+  // one round (and one barrier) per operand.  With two buffers the rounds
+  // alternate between them: a buffer is rewritten two rounds after it was
+  // read, and every work-item has passed the barrier of the round in
+  // between, so its reads are complete.  With one buffer each round after
+  // the first waits at a barrier of its own before it writes.  The number of
+  // rounds follows the layout masks, which are kernel arguments, so every
+  // such barrier is workgroup-uniform.
   int rnd = 0;
 #pragma unroll
   for (int k = 0; k < NI; ++k) {
@@ -390,20 +400,20 @@ __global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
       TI *lds = reinterpret_cast<TI *>(lds_raw[rnd % EW_TILE_BUFS]);
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
-        const int f_ = t + EW_THREADS * i;
-        const int q = f_ & 15, l = f_ >> 4;
+        const unsigned f_ = unsigned(t + NTH * i);
+        const int qq = int(f_ % QR), ll = int(f_ / QR);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          lds[l * P + 4 * q + j] = v[k][i][j];
+          lds[ll * PR + 4 * qq + j] = v[k][i][j];
       }
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
-        const int f_ = t + EW_THREADS * i;
-        const int q = f_ & 15, l = f_ >> 4;
+        const unsigned f_ = unsigned(t + NTH * i);
+        const int q = int(f_ % QC), l = int(f_ / QC);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          v[k][i][j] = lds[(4 * q + j) * P + l];
+          v[k][i][j] = lds[(4 * q + j) * PR + l];
       }
       ++rnd;
     }
@@ -434,31 +444,31 @@ __global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
       ++rnd;
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
-        const int f_ = t + EW_THREADS * i;
-        const int q = f_ & 15, l = f_ >> 4;
+        const unsigned f_ = unsigned(t + NTH * i);
+        const int q = int(f_ % QC), l = int(f_ / QC);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          lds[(4 * q + j) * P + l] = o[m][i][j];
+          lds[(4 * q + j) * PR + l] = o[m][i][j];
       }
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
-        const int f_ = t + EW_THREADS * i;
-        const int q = f_ & 15, l = f_ >> 4;
-        const int64_t r = r0 + 4 * q, c = c0 + l;
+        const unsigned f_ = unsigned(t + NTH * i);
+        const int qq = int(f_ % QR), ll = int(f_ / QR);
+        const int64_t r = r0 + 4 * qq, c = c0 + ll;
         if (r < R && c < C) {
           VecT<TO, 4> w;
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            w.v[j] = lds[l * P + 4 * q + j];
+            w.v[j] = lds[ll * PR + 4 * qq + j];
           vstore<NTL, TO, 4>(p + r + c * sc, w);
         }
       }
     } else if (row_out & (1u << m)) {
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
-        const int f_ = t + EW_THREADS * i;
-        const int q = f_ & 15, l = f_ >> 4;
+        const unsigned f_ = unsigned(t + NTH * i);
+        const int q = int(f_ % QC), l = int(f_ / QC);
         const int64_t r = r0 + l, c = c0 + 4 * q;
         if (r < R && c < C) {
           VecT<TO, 4> w;
@@ -471,8 +481,8 @@ __global__ __launch_bounds__(EW_THREADS) void ew_tile4_kernel(
     } else {
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
-        const int f_ = t + EW_THREADS * i;
-        const int q = f_ & 15, l = f_ >> 4;
+        const unsigned f_ = unsigned(t + NTH * i);
+        const int q = int(f_ % QC), l = int(f_ / QC);
         const int64_t r = r0 + l;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -837,22 +847,61 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       sout.c[m] = L.strides[NI + m][1];
       classify(sout.r[m], sout.c[m], pout.p[m], sizeof(TO), 1u << m, row_out, col_out);
     }
+    // 16-byte tile kernel: TR x TC tiles, TR * TC / 16 work-items.
+    auto tile4 = [&]<int TR, int TC>() {
+      constexpr int64_t NTH = TR * TC / 16;
+      const int64_t tr_n = (R + TR - 1) / TR, tc_n = (C + TC - 1) / TC;
+      const int64_t blocks = tr_n * tc_n;
+      if (blocks * NTH >= (int64_t(1) << 32))
+        return false;
+      const dim3 grid{unsigned(blocks), 1u, 1u};
+      if (ntl)
+        ew_tile4_kernel<TI, TO, NI, NO, true, TR, TC, F>
+            <<<grid, unsigned(NTH), 0, s>>>(pin, sin, row_in, col_in, bcol_in,
+                                            pout, sout, row_out, col_out, R, C,
+                                            tc_n, f);
+      else
+        ew_tile4_kernel<TI, TO, NI, NO, false, TR, TC, F>
+            <<<grid, unsigned(NTH), 0, s>>>(pin, sin, row_in, col_in, bcol_in,
+                                            pout, sout, row_out, col_out, R, C,
+                                            tc_n, f);
+      NT_LAUNCH_CHECK();
+      return true;
+    };
+    if (vec4) {
+      // Tile shape by the streams in each layout, fp32 only (other types
+      // keep 64 x 64 and one instantiation).  Measured on the [4096, 4096]
+      // sweep, alternating with 64 x 64 for every kernel on one MI355X: one
+      // exchanged stream and at least three row-layout streams (the add /
+      // sub / mul backwards, which exchange only the upstream gradient)
+      // +4-6% with 128 x 64 (512-byte exchanged segments); one exchanged
+      // stream and fewer row-layout ones (the unary forwards, the neg
+      // backward) +1.5-9% with 64 x 128, pow -1%; two or more exchanged
+      // streams (binary forwards, unary backwards) were best at 64 x 64.
+      // Whole sweep +0.8%.
+      bool done = false;
+      if constexpr (std::is_same_v<TI, float> && std::is_same_v<TO, float>) {
+        const int n_col = __builtin_popcount(col_in) + __builtin_popcount(col_out);
+        const int n_row = __builtin_popcount(row_in) + __builtin_popcount(row_out);
+        if (n_col == 1 && n_row >= 3)
+          done = tile4.template operator()<128, 64>();
+        else if (n_col == 1)
+          done = tile4.template operator()<64, 128>();
+        else
+          done = tile4.template operator()<64, 64>();
+      } else {
+        done = tile4.template operator()<64, 64>();
+      }
+      if (done)
+        return;
+    }
     const int64_t tiles_r = (R + EW_TILE - 1) / EW_TILE;
     const int64_t tiles_c = (C + EW_TILE - 1) / EW_TILE;
     const int64_t blocks = tiles_r * tiles_c;
-    if (blocks * EW_THREADS < (int64_t(1) << 32)) {
+    if (!vec4 && blocks * EW_THREADS < (int64_t(1) << 32)) {
       const dim3 grid{unsigned(blocks), 1u, 1u};
-      if (vec4 && ntl)
-        ew_tile4_kernel<TI, TO, NI, NO, true, F><<<grid, EW_THREADS, 0, s>>>(
-            pin, sin, row_in, col_in, bcol_in, pout, sout, row_out, col_out, R,
-            C, tiles_c, f);
-      else if (vec4)
-        ew_tile4_kernel<TI, TO, NI, NO, false, F><<<grid, EW_THREADS, 0, s>>>(
-            pin, sin, row_in, col_in, bcol_in, pout, sout, row_out, col_out, R,
-            C, tiles_c, f);
-      else
-        ew_tile_kernel<TI, TO, NI, NO, F><<<grid, EW_THREADS, 0, s>>>(
-            pin, sin, col_in, pout, sout, col_out, R, C, tiles_c, f);
+      ew_tile_kernel<TI, TO, NI, NO, F><<<grid, EW_THREADS, 0, s>>>(
+          pin, sin, col_in, pout, sout, col_out, R, C, tiles_c, f);
       NT_LAUNCH_CHECK();
       return;
     }

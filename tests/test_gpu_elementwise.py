@@ -310,6 +310,43 @@ def test_binary_backward_kernel(gpu, name, op, oop, need, acc):
             assert_bitexact(got, w, f"{name} grad {i}")
 
 
+@pytest.mark.parametrize("shape", [(196, 452), (452, 196), (68, 132), (132, 68),
+                                   (4, 260), (260, 4), (132, 132)])
+def test_tile_shapes_partial_tiles(gpu, shape):
+    """The 16-byte tile kernel's fp32 tile shapes (64 x 64, 128 x 64 and
+    64 x 128, picked by how many streams go through the LDS exchange and how
+    many are read or written straight) on 4-aligned shapes that are not
+    multiples of the tiles, so every launch has partial tiles along both
+    axes.  Cases by stream counts (exchanged / straight): unary forward of a
+    `.T` view (1 / 1), binary forward of two `.T` views (2 / 1), mul
+    backward of `.T` operands into `.T` gradients (1 / 6), neg backward into
+    a `.T` gradient (1 / 2), exp backward with a contiguous saved output
+    (2 / 2) and with a `.T` one (1 / 3), each accumulating; bit-exact."""
+    r = rng(seed_of("tile-shapes", shape))
+    a = r.standard_normal(shape).astype(np.float32)
+    b = r.standard_normal(shape).astype(np.float32)
+    g = r.standard_normal(shape).astype(np.float32)
+    old = [r.standard_normal(shape).astype(np.float32) for _ in range(2)]
+    for op, oop in ((_lib.NEG, O.NEG), (_lib.RELU, O.RELU)):
+        got = host(nt.Tensor._new_contiguous(K.unary(op, dev_T(a), 0.0), shape))
+        assert_bitexact(got, O.unary(oop, a, 0.0), f"unary fwd {op}")
+    got = host(nt.Tensor._new_contiguous(K.binary(_lib.ADD, dev_T(a), dev_T(b)), shape))
+    assert_bitexact(got, O.binary(O.ADD, a, b), "add fwd")
+    tg = [dev_T(old[0]), dev_T(old[1])]
+    K.binary_bwd(_lib.MUL, dev(g), dev_T(a), dev_T(b), True, tg[0], True, tg[1])
+    ga, gb = O.bwd_binary(O.MUL, g, a, b)
+    assert_bitexact(host(tg[0]), O.accumulate(old[0], ga), "mul bwd a")
+    assert_bitexact(host(tg[1]), O.accumulate(old[1], gb), "mul bwd b")
+    t = dev_T(old[0])
+    K.unary_bwd(_lib.NEG, dev(g), None, 0.0, t)
+    assert_bitexact(host(t), O.accumulate(old[0], O.bwd_neg(g)), "neg bwd")
+    y = O.unary(O.EXP, a, 0.0)
+    for saved in (dev(y), dev_T(y)):
+        t = dev_T(old[1])
+        K.unary_bwd(_lib.EXP, dev(g), saved, 0.0, t)
+        assert_bitexact(host(t), O.accumulate(old[1], O.bwd_exp(g, y)), "exp bwd")
+
+
 # ------------------------------------------------------------ config 2 size
 
 
