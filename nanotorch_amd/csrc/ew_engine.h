@@ -877,8 +877,9 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       // +4-6% with 128 x 64 (512-byte exchanged segments); one exchanged
       // stream and fewer row-layout ones (the unary forwards, the neg
       // backward) +1.5-9% with 64 x 128, pow -1%; two or more exchanged
-      // streams (binary forwards, unary backwards) were best at 64 x 64.
-      // Whole sweep +0.8%.
+      // streams (binary forwards, unary backwards) were best at 64 x 64
+      // (the whole sweep 0.2 / 0.7 / 2.3% slower with 64 x 128, 128 x 64 or
+      // 128 x 128 for them).  Whole sweep +0.8%.
       bool done = false;
       if constexpr (std::is_same_v<TI, float> && std::is_same_v<TO, float>) {
         const int n_col = __builtin_popcount(col_in) + __builtin_popcount(col_out);
