@@ -285,3 +285,52 @@ def test_split_slices_back_to_back(gpu):
         want_cnt = (a == np.expand_dims(want_max, axes)).sum(axis=axes).astype(np.int32)
         assert_bitexact(host(nt.Tensor._new_contiguous(cnt, kshape)), want_cnt, "count " + tag)
         assert_bitexact(host(nt.Tensor._new_contiguous(am, kshape)), O.reduce(O.R_ARGMIN, a, axes), "argmin " + tag)
+
+
+@pytest.mark.parametrize("shape,axes", [
+    ((5, 50000), (1,)),       # row kernel, slices split over segments
+    ((64, 4096), (1,)),       # row kernel, one workgroup per slice
+    ((1 << 20,), (0,)),       # full reduction
+    ((4096, 1030), (0,)),     # column walk (wide blocks and a ragged edge)
+    ((37, 9, 401), (0, 2)),   # generic kernel
+])
+def test_select_special_values(gpu, shape, axes):
+    """Max / min / argmax / argmin and tie counts over +-inf, the neutral
+    values -FLT_MAX / FLT_MAX themselves, signed zeros (the value of the
+    first extremum is returned, bit for bit) and NaN.  Slices made only of
+    -inf (max) or +inf (min) give the neutral value and index INT64_MAX, as
+    the reference's loop does.  NaN never wins and is never counted (a
+    documented deviation: the reference's result depends on where NaNs
+    sit), which is the reference's result with each NaN replaced by -inf
+    (max) or +inf (min), so the oracle runs on that array."""
+    r = rng(seed_of("special", shape, axes))
+    fmax = np.finfo(np.float32).max
+    palette = np.array([np.nan, np.inf, -np.inf, -fmax, fmax, 0.0, -0.0, 1.0, -1.0], np.float32)
+    a = r.standard_normal(shape).astype(np.float32)
+    pick = r.random(shape) < 0.3
+    a[pick] = palette[r.integers(0, len(palette), int(pick.sum()))]
+    # whole slices of special values along the reduced axes (not for a full
+    # reduction, whose one slice is the whole tensor)
+    lead = [slice(None)] * a.ndim
+    kept = [d for d in range(a.ndim) if d not in axes]
+    specials = [[-np.inf], [np.inf], [np.nan], [0.0, -0.0], [-0.0, 0.0], [-np.inf, -fmax], [np.inf, fmax]]
+    for i, vals in enumerate(specials if kept else []):
+        idx = list(lead)
+        for d in kept:
+            idx[d] = i % a.shape[d]
+        sub = a[tuple(idx)]
+        sub[...] = np.asarray(vals, np.float32)[r.integers(0, len(vals), sub.shape)]
+    x = dev(a)
+    kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+    for op, oop, aop, argop, fill in ((_lib.R_MAX, O.R_MAX, O.R_ARGMAX, _lib.R_ARGMAX, -np.inf),
+                                      (_lib.R_MIN, O.R_MIN, O.R_ARGMIN, _lib.R_ARGMIN, np.inf)):
+        ref_in = np.where(np.isnan(a), np.float32(fill), a)
+        want = O.reduce(oop, ref_in, axes)
+        v, idx, cnt = K.reduce(op, x, axes, nt.float32, want_aux=True)
+        assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), want, f"value {op}")
+        want_idx = O.reduce(aop, ref_in, axes)
+        assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), want_idx, f"index {op}")
+        got_arg = host(nt.Tensor._new_contiguous(K.reduce(argop, x, axes, nt.int64), kshape))
+        assert_bitexact(got_arg, want_idx, f"arg {op}")
+        want_cnt = (ref_in == np.expand_dims(want, axes)).sum(axis=axes).astype(np.int32)
+        assert_bitexact(host(nt.Tensor._new_contiguous(cnt, kshape)), want_cnt, f"count {op}")
