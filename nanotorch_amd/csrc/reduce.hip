@@ -174,6 +174,37 @@ template <class O, bool IS_MAX> struct SelAcc32 {
     c = cn;
     v = b ? x : v;
   }
+  // N elements at indices jb + off[0] < jb + off[1] < ..., in one step with
+  // the result of N add() calls.  m is the chunk's best, taken with a
+  // strict comparison in index order from the neutral value: it is the
+  // first best element's value (a zero keeps the first zero's sign), and
+  // NaN and elements beyond the neutral value never count.  cc counts the
+  // elements equal to m and jf is the first one's offset.  Then, as add()
+  // would have: a better m replaces the state, an equal one adds its count,
+  // and an equal one meeting an empty state (the neutral value met its
+  // equal) is taken with its first index.
+  template <int N>
+  __device__ __forceinline__ void add_chunk(const O (&x)[N], int32_t jb,
+                                            const int32_t (&off)[N]) {
+    O m = IS_MAX ? std::numeric_limits<O>::lowest()
+                 : std::numeric_limits<O>::max();
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+      m = SelAcc<O, IS_MAX>::better(x[k], m) ? x[k] : m;
+    int32_t cc = 0, jf = 0;
+#pragma unroll
+    for (int k = N - 1; k >= 0; --k) {
+      const bool e = x[k] == m;
+      cc += e ? 1 : 0;
+      jf = e ? off[k] : jf;
+    }
+    const bool b = SelAcc<O, IS_MAX>::better(m, v);
+    const bool eq = m == v;
+    const bool take = b || (eq && c == 0);
+    v = take ? m : v;
+    j = take ? jb + jf : j;
+    c = take ? cc : c + (eq ? cc : 0);
+  }
 };
 
 template <class Acc> struct IsSel : std::false_type {};
@@ -280,11 +311,13 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
   // and widen it once at the end.
   using LA = std::conditional_t<IDX32, typename ColLocal<Acc>::type, Acc>;
   using IT = std::conditional_t<IDX32, int32_t, int64_t>;
-  // Max/min: one accumulator per vector lane (element i of every vector
-  // goes to a[i]), so the per-element select chains are independent; each
-  // still sees its elements in increasing j, and the merge below keeps the
-  // smallest index on ties, so the result is the single-chain one.  Sums
-  // keep one chain (their rounding is order-dependent).
+  // Max/min: the main loop feeds a[0] whole chunks (32-bit index) or, with
+  // 64-bit indices, one accumulator per vector lane (element i of every
+  // vector goes to a[i]) so the per-element select chains are independent;
+  // the tail goes per lane too.  Each accumulator sees its elements in
+  // increasing j, and the merge below keeps the smallest index on ties, so
+  // the result is the single-chain one.  Sums keep one chain (their
+  // rounding is order-dependent).
   constexpr int NA = IsSel<Acc>::value ? VEC : 1;
   LA a[NA];
 #pragma unroll
@@ -302,11 +335,29 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
     for (int u = 0; u < UR; ++u)
       v[u] = vload<true, T, VEC>(row + j + u * step);
     const IT jb = IDX32 ? IT(j - j0) : IT(j);
+    if constexpr (IsSel<Acc>::value && IDX32) {
+      // max/min: the UR * VEC elements as one chunk, in index order
+      // (add_chunk: 6.6 VALU instructions per element against 8.5 for
+      // per-element updates; full max/min 0.68-0.71 -> 0.73-0.75 of peak,
+      // along a trailing axis unchanged; one chunk of UR elements per
+      // vector lane took 10)
+      O xs[UR * VEC];
+      int32_t off[UR * VEC];
 #pragma unroll
-    for (int u = 0; u < UR; ++u)
+      for (int u = 0; u < UR; ++u)
 #pragma unroll
-      for (int i = 0; i < VEC; ++i)
-        a[i % NA].add(static_cast<O>(v[u].v[i]), jb + IT(u * step + i));
+        for (int i = 0; i < VEC; ++i) {
+          xs[u * VEC + i] = static_cast<O>(v[u].v[i]);
+          off[u * VEC + i] = u * int32_t(step) + i;
+        }
+      a[0].add_chunk(xs, int32_t(jb), off);
+    } else {
+#pragma unroll
+      for (int u = 0; u < UR; ++u)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+          a[i % NA].add(static_cast<O>(v[u].v[i]), jb + IT(u * step + i));
+    }
   }
   for (; j < j1; j += step) {
     const IT jb = IDX32 ? IT(j - j0) : IT(j);
