@@ -20,8 +20,9 @@
 //              segments whose partials a second kernel combines in order.
 //  * column -- the kept axis is the contiguous one (e.g. axis=0 of a
 //              row-major matrix): each lane owns 4 adjacent columns and walks
-//              rows, so every wave load is 1 KB contiguous; rows are split
-//              across S workgroups and a second kernel combines partials.
+//              rows, so every wave load is 1 KB contiguous; rows are dealt
+//              round-robin to S workgroups and a second kernel combines
+//              partials.
 //  * generic-- anything else: one workgroup per (slice, segment), elements
 //              located by multiply-high unravel of j over the drop view.
 // Max/min carry (value, first j, count of elements equal to the extremum);
@@ -39,17 +40,27 @@ namespace nt {
 constexpr int RED_THREADS = 256;
 constexpr int RED_WAVES = RED_THREADS / 64;
 
-// Column-walk shape (reduce_col_kernel): rows in flight per work-item, wave
-// columns per workgroup on wide tensors, workgroups per CU for sums and for
-// max/min.
+// Row kernel: 16-byte loads in flight per work-item, workgroups per CU for
+// slices split over several workgroups.
 #ifndef NT_ROW_UR
 #define NT_ROW_UR 4
 #endif
 #ifndef NT_ROW_WG_PER_CU
 #define NT_ROW_WG_PER_CU 2 // measured: full sums 6.6 -> 6.8 TB/s against 4
 #endif
+// Column walk (reduce_col_kernel): rows per group for sums and for max/min,
+// wave columns per workgroup on wide tensors, workgroups per CU for sums and
+// for max/min, the pipelined walk (the next group's loads issued before this
+// group's arithmetic) and rows dealt round-robin to the segments.  Measured
+// on [8192, 8192] axis 0 with all of these: sums 0.81-0.83 of peak at 4 rows
+// a group (0.79 at 6 and 0.79-0.81 at 8 without the pipeline, 0.75 at 6 with
+// it), max/min 0.78-0.79 at 4 (0.73 at 6, 0.53 without the pipeline), two or
+// four workgroups per CU 0.66 / 0.49 for max/min and 0.73 / 0.58 for sums.
 #ifndef NT_COL_UR
-#define NT_COL_UR 6 // measured: max/min axis 0 4.7 -> 5.1 TB/s against 8, sums equal
+#define NT_COL_UR 4
+#endif
+#ifndef NT_COL_UR_SEL
+#define NT_COL_UR_SEL 4
 #endif
 #ifndef NT_COL_WC
 #define NT_COL_WC 4
@@ -57,20 +68,18 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 #ifndef NT_COL_WG_SUM
 #define NT_COL_WG_SUM 1
 #endif
-// Max/min column walks issue the next UR rows' loads before the current
-// rows' selects (measured on [8192, 8192] axis 0: 0.60 -> 0.675 of peak at one
-// workgroup per CU; without it two workgroups per CU were best).
-#ifndef NT_COMBINE_WIDE
-#define NT_COMBINE_WIDE 256 // work-items per slice when at most 64 slices (1024: same or slower)
+#ifndef NT_COL_WG_SEL
+#define NT_COL_WG_SEL 1
 #endif
 #ifndef NT_COL_PIPE
 #define NT_COL_PIPE 1
 #endif
-#ifndef NT_COL_UR_SEL
-#define NT_COL_UR_SEL 4 // pipelined max/min walk: 0.70 of peak at 4 rows a group, 0.65-0.68 at 6, 0.66-0.68 at 3, 0.69 at 5
+#ifndef NT_COL_INTERLEAVE
+#define NT_COL_INTERLEAVE 1
 #endif
-#ifndef NT_COL_WG_SEL
-#define NT_COL_WG_SEL 1 // measured with NT_COL_PIPE: 0.675 / 0.51 of peak at 1 / 2
+// Work-items per slice of the second pass when there are at most 64 slices.
+#ifndef NT_COMBINE_WIDE
+#define NT_COMBINE_WIDE 256 // 1024: same or slower
 #endif
 
 // ------------------------------------------------------------ accumulators
@@ -213,15 +222,16 @@ struct IsSel<SelAcc<O, IS_MAX>> : std::true_type {};
 
 template <class Acc> struct ColLocal {
   using type = Acc;
-  __device__ static Acc widen(const Acc &a, int64_t) { return a; }
+  __device__ static Acc widen(const Acc &a, int64_t, int64_t = 1) { return a; }
 };
 template <class O, bool IS_MAX> struct ColLocal<SelAcc<O, IS_MAX>> {
   using type = SelAcc32<O, IS_MAX>;
-  __device__ static SelAcc<O, IS_MAX> widen(const type &a, int64_t j0) {
+  __device__ static SelAcc<O, IS_MAX> widen(const type &a, int64_t j0,
+                                            int64_t mult = 1) {
     SelAcc<O, IS_MAX> r;
     r.v = a.v;
     // c == 0: no element was taken, the index stays the neutral INT64_MAX
-    r.j = a.c == 0 ? std::numeric_limits<int64_t>::max() : j0 + a.j;
+    r.j = a.c == 0 ? std::numeric_limits<int64_t>::max() : j0 + a.j * mult;
     r.c = a.c;
     return r;
   }
@@ -394,7 +404,7 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
 
 // x is [D, K] with K contiguous (stride 1) and row stride sd.  Block
 // (bx, s) covers columns [bx * CB, +CB), CB = 64 * VEC * WC, and rows
-// [s * seg, ..): WC waves stand side by side (lane l owns VEC adjacent
+// s, s + S, s + 2S, ...: WC waves stand side by side (lane l owns VEC adjacent
 // columns, so a block reads CB * sizeof(T) contiguous bytes of each row) and
 // the RED_WAVES / WC wave rows interleave the segment's rows, UR rows in
 // flight per lane.  Partials go to partial[s * K + k] (coalesced), combined
@@ -411,10 +421,22 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
   const int s = blockIdx.y;
   const int64_t k0 =
       int64_t(blockIdx.x) * CB + int64_t(wc) * 64 * VEC + int64_t(lane) * VEC;
-  const int64_t j0 = int64_t(s) * seg;
+#if NT_COL_INTERLEAVE
+  // Segment s takes rows s, s + S, s + 2S, ... (relative row r is row
+  // s + r S), so all workgroups walk one window of rows down the tensor
+  // together.  Contiguous row ranges per segment spread the concurrent
+  // reads over S distant parts of the tensor: axis-0 max / min / sum of
+  // [8192, 8192] ran at 0.69-0.72 of peak that way, 0.78-0.79 interleaved.
+  const int64_t j0 = s, jm = S;
+  const int32_t nr = s < D ? int32_t((D - s + S - 1) / S) : 0;
+  const T *base = x + j0 * sd + k0;
+  sd *= S;
+#else
+  const int64_t j0 = int64_t(s) * seg, jm = 1;
   // rows of this segment, relative to j0 (seg < 2^31, checked by the host)
   const int32_t nr = int32_t((j0 + seg < D ? j0 + seg : D) - j0);
   const T *base = x + j0 * sd + k0;
+#endif
   using LA = typename ColLocal<Acc>::type;
   LA la[VEC];
 #pragma unroll
@@ -424,9 +446,9 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
   if (k0 + VEC <= K) {
     int32_t jr = wr;
 #if NT_COL_PIPE
-    // Groups of UR rows (g-th group: rows wr + g*UR*WR + u*WR).  Max/min
-    // spend long enough on a group's selects that a wave would otherwise
-    // leave the memory pipe idle meanwhile: the next group's loads go out
+    // Groups of UR rows (g-th group: rows wr + g*UR*WR + u*WR).  A wave
+    // would otherwise leave the memory pipe idle while it works through a
+    // group (max/min selects above all): the next group's loads go out
     // before this group's arithmetic, alternating two register sets (a copy
     // between them would wait for the loads in flight).  The last prefetch
     // re-reads the last group (clamped index, in bounds) and is discarded.
@@ -437,7 +459,7 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
     const int32_t ng = nru - 1 - wru - (UR - 1) * WR >= 0
                            ? (nru - 1 - wru - (UR - 1) * WR) / GR + 1
                            : 0;
-    if (IsSel<Acc>::value && ng > 0) {
+    if (ng > 0) {
       V va[UR], vb[UR];
       const int64_t rs = int64_t(WR) * sd, gs = int64_t(GR) * sd;
       const T *pa = base + int64_t(wru) * sd; // group 0
@@ -497,7 +519,7 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
   Acc a[VEC];
 #pragma unroll
   for (int i = 0; i < VEC; ++i)
-    a[i] = ColLocal<Acc>::widen(la[i], j0);
+    a[i] = ColLocal<Acc>::widen(la[i], j0, jm);
   if constexpr (WR > 1) {
     // Wave rows of one column group merge in wave-row order.
 #pragma unroll
