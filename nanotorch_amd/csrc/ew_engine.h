@@ -14,12 +14,11 @@
 //               contiguous are read straight; operands contiguous along the
 //               other axis (e.g. `x.T`) are staged through a padded LDS tile
 //               so both the global read and the global write stay
-//               coalesced.  Outputs
-//               laid out that way go back through the same LDS tile.  The
-//               tile walks whichever orientation exchanges less.  With
-//               4-aligned sizes and strides every access is a 16-byte vector
-//               (ew_tile4_kernel); otherwise element accesses
-//               (ew_tile_kernel).
+//               coalesced.  Outputs laid out that way go back through the
+//               same LDS tile.  The tile walks whichever orientation
+//               exchanges less.  With 4-aligned sizes and strides every
+//               access is a 16-byte vector (ew_tile4_kernel); otherwise
+//               element accesses (ew_tile_kernel).
 //  * generic -- anything else (up to 8 dims): per-element unravel with
 //               multiply-high division when the index fits in 32 bits.
 //
@@ -68,7 +67,6 @@ constexpr int EW_TILE_PAD = 65;
 #define NT_TILE_LDS_BUFS 1
 #endif
 constexpr int EW_TILE_BUFS = NT_TILE_LDS_BUFS;
-
 static_assert(EW_TILE_BUFS == 1 || EW_TILE_BUFS == 2, "one or two tile buffers");
 
 template <class T, int N> struct PtrPack {
@@ -289,19 +287,6 @@ __global__ __launch_bounds__(NT_ROWS_THREADS) void ew_rows_kernel(
 
 // --------------------------------------------------------------- tile2d x4
 
-// TR x TC tile (TR rows by TC columns of the iteration space) with 4-element
-// vector accesses (16 B for fp32), TR * TC / 16 work-items.
-//  * ROW operands (unit column stride) are read/written straight: TC / 4
-//    work-items cover one row segment of TC elements (256 bytes of fp32 at
-//    TC = 64).
-//  * COL operands (unit row stride, e.g. `x.T`) are read as column segments
-//    of TR elements, 4 consecutive rows per work-item, and exchanged through
-//    a [col][row] LDS tile whose rows are padded to TR + 1 elements (a
-//    wave's accesses spread over the banks).  Outputs of that layout take
-//    the reverse path.
-//  * Other operands (stride-0 broadcasts, general strides) are read per
-//    element in the owner (ROW) layout.
-// All global loads of all inputs are issued before the first LDS exchange.
 // Tile (tr, tc) of workgroup b in a tiles_r x tiles_c grid (fewer than 2^24
 // tiles), in diagonal order: consecutive workgroups take consecutive tile
 // columns, each one tile row further on, tr = (b / tiles_c + tc) mod tiles_r.
@@ -321,9 +306,22 @@ __device__ __forceinline__ void diagonal_tile(uint32_t b, int64_t tiles_r,
   tr = (q + c) % nr;
 }
 
+// TR x TC tile (TR rows by TC columns of the iteration space) with 4-element
+// vector accesses (16 B for fp32), TR * TC / 16 work-items.
+//  * ROW operands (unit column stride) are read/written straight: TC / 4
+//    work-items cover one row segment of TC elements (256 bytes of fp32 at
+//    TC = 64).
+//  * COL operands (unit row stride, e.g. `x.T`) are read as column segments
+//    of TR elements, 4 consecutive rows per work-item, and exchanged through
+//    a [col][row] LDS tile whose rows are padded to TR + 1 elements (a
+//    wave's accesses spread over the banks).  Outputs of that layout take
+//    the reverse path.
+//  * Other operands (stride-0 broadcasts, general strides) are read per
+//    element in the owner (ROW) layout.
+// All global loads of all inputs are issued before the first LDS exchange.
 template <class TI, class TO, int NI, int NO, bool NTL, int TR, int TC,
           class F>
-__global__ __launch_bounds__(TR *TC / 16) void ew_tile4_kernel(
+__global__ __launch_bounds__(TR * TC / 16) void ew_tile4_kernel(
     PtrPack<const TI, NI> in, Strides2<NI> sin, uint32_t row_in,
     uint32_t col_in, uint32_t bcol_in, PtrPack<TO, NO> out, Strides2<NO> sout,
     uint32_t row_out, uint32_t col_out, int64_t R, int64_t C, int64_t tiles_c,
