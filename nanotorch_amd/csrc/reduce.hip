@@ -77,10 +77,11 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 #ifndef NT_COL_INTERLEAVE
 #define NT_COL_INTERLEAVE 1
 #endif
-// Work-items per slice of the second pass when there are at most 64 slices.
+// Workgroups per CU of the 2-D max/min backward.
 #ifndef NT_SEL2D_WG
-#define NT_SEL2D_WG 32 // workgroups per CU of the 2-D max/min backward (8: 0.70-0.74 of peak against 0.80-0.81)
+#define NT_SEL2D_WG 32 // 8: 0.70-0.74 of peak against 0.80-0.81
 #endif
+// Work-items per slice of the second pass when there are at most 64 slices.
 #ifndef NT_COMBINE_WIDE
 #define NT_COMBINE_WIDE 256 // 1024: same or slower
 #endif
@@ -407,11 +408,11 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
 
 // x is [D, K] with K contiguous (stride 1) and row stride sd.  Block
 // (bx, s) covers columns [bx * CB, +CB), CB = 64 * VEC * WC, and rows
-// s, s + S, s + 2S, ...: WC waves stand side by side (lane l owns VEC adjacent
-// columns, so a block reads CB * sizeof(T) contiguous bytes of each row) and
-// the RED_WAVES / WC wave rows interleave the segment's rows, UR rows in
-// flight per lane.  Partials go to partial[s * K + k] (coalesced), combined
-// by reduce_col_combine_kernel.
+// s, s + S, s + 2S, ...: WC waves stand side by side (lane l owns VEC
+// adjacent columns, so a block reads CB * sizeof(T) contiguous bytes of each
+// row) and the RED_WAVES / WC wave rows interleave the segment's rows, UR
+// rows in flight per lane.  Partials go to partial[s * K + k] (coalesced),
+// combined by reduce_col_combine_kernel.
 template <class T, class O, class Acc, int VEC, int WC, int UR, int MODE>
 __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
     const T *__restrict__ x, int64_t K, int64_t D, int64_t sd, int64_t seg,
