@@ -321,7 +321,8 @@ def test_tile_shapes_partial_tiles(gpu, shape):
     `.T` view (1 / 1), binary forward of two `.T` views (2 / 1), mul
     backward of `.T` operands into `.T` gradients (1 / 6), neg backward into
     a `.T` gradient (1 / 2), exp backward with a contiguous saved output
-    (2 / 2) and with a `.T` one (1 / 3), each accumulating; bit-exact."""
+    (2 / 2) and with a `.T` one (1 / 3), each accumulating, and binary ops of
+    a `.T` view with broadcast rows, columns and scalars; bit-exact."""
     r = rng(seed_of("tile-shapes", shape))
     a = r.standard_normal(shape).astype(np.float32)
     b = r.standard_normal(shape).astype(np.float32)
@@ -345,6 +346,20 @@ def test_tile_shapes_partial_tiles(gpu, shape):
         t = dev_T(old[1])
         K.unary_bwd(_lib.EXP, dev(g), saved, 0.0, t)
         assert_bitexact(host(t), O.accumulate(old[1], O.bwd_exp(g, y)), "exp bwd")
+    # a `.T` operand beside a broadcast row (bias), a broadcast column and a
+    # scalar, in both operand positions (one exchanged stream)
+    row = r.uniform(0.5, 2, shape[1:]).astype(np.float32)
+    col = r.uniform(0.5, 2, (shape[0], 1)).astype(np.float32)
+    sc = np.array([[1.75]], np.float32)
+    for other, onp in ((dev(row).expand(*shape), np.broadcast_to(row, shape)),
+                       (dev(col).expand(*shape), np.broadcast_to(col, shape)),
+                       (dev(sc).expand(*shape), np.broadcast_to(sc, shape))):
+        onp = np.ascontiguousarray(onp)
+        for op, oop in ((_lib.ADD, O.ADD), (_lib.DIV, O.DIV)):
+            got = host(nt.Tensor._new_contiguous(K.binary(op, dev_T(a), other), shape))
+            assert_bitexact(got, O.binary(oop, a, onp), f"op {op} .T with broadcast")
+            got = host(nt.Tensor._new_contiguous(K.binary(op, other, dev_T(a)), shape))
+            assert_bitexact(got, O.binary(oop, onp, a), f"op {op} broadcast with .T")
 
 
 # ------------------------------------------------------------ config 2 size
