@@ -577,6 +577,34 @@ def bench_copy_reference(iters: int = 8) -> dict:
             "bytes": 8 * n}
 
 
+def bench_copy_sweep_size(iters: int = 16) -> dict:
+    """The same copy at the sweep's size: 2^24 fp32 elements in, 2^24 out
+    (the bytes of one contiguous unary forward), contiguous and from a `.T`
+    view of a [4096, 4096] array (the bytes and layout of a transposed
+    unary forward), over 8 rotating pairs (1 GB, not Infinity-Cache
+    resident).  The ceiling a launch of that length reaches, ramp-up and
+    drain included, for the sweep's contiguous and transposed kernels."""
+    n = 1 << 24
+    side = 1 << 12
+    pairs = [(_fresh((side, side)), _fresh((side, side))) for _ in range(8)]
+    out = {}
+    for name, src in (("contiguous", lambda a: a), ("transposed", lambda a: a.T)):
+        for a, b in pairs:
+            K.copy_view(src(a), b)
+        e0, e1 = _lib.Event(), _lib.Event()
+        e0.record()
+        for it in range(iters):
+            a, b = pairs[it % 8]
+            K.copy_view(src(a), b)
+        e1.record()
+        nt.sync()
+        ms = e0.elapsed_ms(e1) / iters
+        gbs = 8 * n / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 5), "GB/s": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": 8 * n}
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline
 
 
@@ -1212,6 +1240,14 @@ def main() -> int:
     copy_ref = bench_copy_reference()
     copy_ref["sweep_vs_copy"] = round(value / copy_ref["GB/s"], 4)
     line["parts"]["copy_reference"] = copy_ref
+    # the sweep's unary forwards against a copy of their own size and layout
+    small = bench_copy_sweep_size()
+    for lay, key in (("contig", "contiguous"), ("transposed", "transposed")):
+        ks = [k for k in ew["per_kernel"] if k.endswith(f"|{lay}|fwd")
+              and k.split("|")[0] not in ("add", "sub", "mul", "truediv")]
+        mean = sum(ew["per_kernel"][k]["GB/s"] for k in ks) / len(ks)
+        small[key]["unary_fwd_vs_copy"] = round(mean / small[key]["GB/s"], 4)
+    line["parts"]["copy_reference_sweep_size"] = small
     if "red" in parts:
         line["parts"]["reductions"] = bench_reductions()
     if "mm" in parts:
