@@ -50,12 +50,13 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 #endif
 // Column walk (reduce_col_kernel): rows per group for sums and for max/min,
 // wave columns per workgroup on wide tensors, workgroups per CU for sums and
-// for max/min, the pipelined walk (the next group's loads issued before this
-// group's arithmetic) and rows dealt round-robin to the segments.  Measured
-// on [8192, 8192] axis 0 with all of these: sums 0.81-0.83 of peak at 4 rows
-// a group (0.79 at 6 and 0.79-0.81 at 8 without the pipeline, 0.75 at 6 with
-// it), max/min 0.78-0.79 at 4 (0.73 at 6, 0.53 without the pipeline), two or
-// four workgroups per CU 0.66 / 0.49 for max/min and 0.73 / 0.58 for sums.
+// for max/min, and the pipelined walk (the next group's loads issued before
+// this group's arithmetic); rows are dealt round-robin to the segments.
+// Measured on [8192, 8192] axis 0 with all of these: sums 0.81-0.83 of peak
+// at 4 rows a group (0.79 at 6 and 0.79-0.81 at 8 without the pipeline,
+// 0.75 at 6 with it), max/min 0.78-0.79 at 4 (0.73 at 6, 0.53 without the
+// pipeline), two or four workgroups per CU 0.66 / 0.49 for max/min and
+// 0.73 / 0.58 for sums.
 #ifndef NT_COL_UR
 #define NT_COL_UR 4
 #endif
@@ -73,9 +74,6 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 #endif
 #ifndef NT_COL_PIPE
 #define NT_COL_PIPE 1
-#endif
-#ifndef NT_COL_INTERLEAVE
-#define NT_COL_INTERLEAVE 1
 #endif
 // Workgroups per CU of the 2-D max/min backward.
 #ifndef NT_SEL2D_WG
@@ -415,8 +413,8 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_row_kernel(
 // combined by reduce_col_combine_kernel.
 template <class T, class O, class Acc, int VEC, int WC, int UR, int MODE>
 __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
-    const T *__restrict__ x, int64_t K, int64_t D, int64_t sd, int64_t seg,
-    int S, Acc *partial, RedOut<MODE> out) {
+    const T *__restrict__ x, int64_t K, int64_t D, int64_t sd, int S,
+    Acc *partial, RedOut<MODE> out) {
   constexpr int WR = RED_WAVES / WC;
   constexpr int CB = 64 * VEC * WC;
   __shared__ Acc lds[WR > 1 ? RED_WAVES : 1][64 * VEC];
@@ -425,22 +423,16 @@ __global__ __launch_bounds__(RED_THREADS) void reduce_col_kernel(
   const int s = blockIdx.y;
   const int64_t k0 =
       int64_t(blockIdx.x) * CB + int64_t(wc) * 64 * VEC + int64_t(lane) * VEC;
-#if NT_COL_INTERLEAVE
   // Segment s takes rows s, s + S, s + 2S, ... (relative row r is row
-  // s + r S), so all workgroups walk one window of rows down the tensor
-  // together.  Contiguous row ranges per segment spread the concurrent
-  // reads over S distant parts of the tensor: axis-0 max / min / sum of
-  // [8192, 8192] ran at 0.69-0.72 of peak that way, 0.78-0.79 interleaved.
+  // s + r S; D < 2^31, checked by the host), so all workgroups walk one
+  // window of rows down the tensor together.  Contiguous row ranges per
+  // segment spread the concurrent reads over S distant parts of the
+  // tensor: axis-0 max / min / sum of [8192, 8192] ran at 0.69-0.72 of
+  // peak that way, 0.78-0.79 round-robin.
   const int64_t j0 = s, jm = S;
   const int32_t nr = s < D ? int32_t((D - s + S - 1) / S) : 0;
   const T *base = x + j0 * sd + k0;
   sd *= S;
-#else
-  const int64_t j0 = int64_t(s) * seg, jm = 1;
-  // rows of this segment, relative to j0 (seg < 2^31, checked by the host)
-  const int32_t nr = int32_t((j0 + seg < D ? j0 + seg : D) - j0);
-  const T *base = x + j0 * sd + k0;
-#endif
   using LA = typename ColLocal<Acc>::type;
   LA la[VEC];
 #pragma unroll
@@ -851,16 +843,16 @@ void run_reduce(const nt_view *x, const RedPlan &p, RedOut<MODE> out,
     const dim3 grid{unsigned(bx), unsigned(S), 1u};
     if (aligned && wc == WC)
       reduce_col_kernel<T, O, Acc, VEC, WC, UR, MODE>
-          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
+          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, int(S), partial, out);
     else if (aligned)
       reduce_col_kernel<T, O, Acc, VEC, 1, UR, MODE>
-          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
+          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, int(S), partial, out);
     else if (wc == WC)
       reduce_col_kernel<T, O, Acc, 1, WC, UR, MODE>
-          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
+          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, int(S), partial, out);
     else
       reduce_col_kernel<T, O, Acc, 1, 1, UR, MODE>
-          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, seg, int(S), partial, out);
+          <<<grid, RED_THREADS, 0, st>>>(xp, K, D, sd, int(S), partial, out);
     NT_LAUNCH_CHECK();
     if (S > 1) {
       reduce_col_combine_kernel<O, Acc, MODE>
