@@ -81,7 +81,7 @@ constexpr int RED_WAVES = RED_THREADS / 64;
 #endif
 // Work-items per slice of the second pass when there are at most 64 slices.
 #ifndef NT_COMBINE_WIDE
-#define NT_COMBINE_WIDE 256 // 1024: same or slower
+#define NT_COMBINE_WIDE 256 // 1024: same or slower; 64 or 128 with 8 loads in flight: slower
 #endif
 
 // ------------------------------------------------------------ accumulators
