@@ -362,6 +362,37 @@ def test_tile_shapes_partial_tiles(gpu, shape):
             assert_bitexact(got, O.binary(oop, onp, a), f"op {op} broadcast with .T")
 
 
+@pytest.mark.parametrize("dtype", [np.float64, np.int32, np.int64])
+def test_tile_kernel_other_dtypes(gpu, dtype):
+    """The 16-byte tile kernel for non-fp32 element types (64 x 64 tiles,
+    vectors of four 8- or 4-byte elements) on 4-aligned shapes with partial
+    tiles: binary ops and negation of `.T` views, comparisons, and casts
+    from a `.T` view to another type; bit-exact."""
+    r = rng(seed_of("tile-dtypes", np.dtype(dtype).name))
+    shape = (132, 196)
+    if np.issubdtype(dtype, np.integer):
+        a = r.integers(-1000, 1000, shape).astype(dtype)
+        b = r.integers(-1000, 1000, shape).astype(dtype)
+    else:
+        a = r.standard_normal(shape).astype(dtype)
+        b = r.standard_normal(shape).astype(dtype)
+    for op, oop in ((_lib.ADD, O.ADD), (_lib.SUB, O.SUB), (_lib.MUL, O.MUL)):
+        got = host(nt.Tensor._new_contiguous(K.binary(op, dev_T(a), dev_T(b)), shape))
+        assert_bitexact(got, O.binary(oop, a, b), f"{op} .T .T")
+        got = host(nt.Tensor._new_contiguous(K.binary(op, dev_T(a), dev(b)), shape))
+        assert_bitexact(got, O.binary(oop, a, b), f"{op} .T contiguous")
+    got = host(nt.Tensor._new_contiguous(K.unary(_lib.NEG, dev_T(a), 0.0), shape))
+    assert_bitexact(got, O.unary(O.NEG, a, 0.0), "neg .T")
+    got = host(nt.Tensor._new_contiguous(K.binary(_lib.GT, dev_T(a), dev(b)), shape))
+    assert_bitexact(got, a > b, "gt .T")
+    for dst in (np.float32, np.float64, np.int64):
+        if np.dtype(dst) == np.dtype(dtype):
+            continue
+        out = dev(np.zeros(shape, dst))
+        K.copy_view(dev_T(a), out)
+        assert_bitexact(host(out), O.cast(a, dst), f"cast .T {np.dtype(dtype).name}->{np.dtype(dst).name}")
+
+
 # ------------------------------------------------------------ config 2 size
 
 
