@@ -334,3 +334,25 @@ def test_select_special_values(gpu, shape, axes):
         assert_bitexact(got_arg, want_idx, f"arg {op}")
         want_cnt = (ref_in == np.expand_dims(want, axes)).sum(axis=axes).astype(np.int32)
         assert_bitexact(host(nt.Tensor._new_contiguous(cnt, kshape)), want_cnt, f"count {op}")
+
+
+@pytest.mark.parametrize("shape,axes", [((3000, 1030), (0,)), ((3, 200003), (1,)), ((1 << 19,), (0,))])
+def test_float64_split_walks(gpu, shape, axes):
+    """fp64 reductions long enough to be split over several workgroups: the
+    column walk's round-robin rows and the row kernel's round-robin max/min
+    chunks and contiguous sum ranges, with 32-byte vectors; sums within the
+    fp64 bound, max/min values, indices and counts exact (integer-valued
+    data: many ties)."""
+    r = rng(seed_of("f64-split", shape, axes))
+    a = r.integers(-20, 21, shape).astype(np.float64)
+    x = dev(a)
+    kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+    got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, axes, nt.float64), kshape))
+    assert_bitexact(got, a.sum(axis=axes), "f64 sum")  # integers: exact
+    for op, oop, aop in ((_lib.R_MAX, O.R_MAX, O.R_ARGMAX), (_lib.R_MIN, O.R_MIN, O.R_ARGMIN)):
+        v, idx, cnt = K.reduce(op, x, axes, nt.float64, want_aux=True)
+        want = O.reduce(oop, a, axes)
+        assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), want, f"f64 {op}")
+        assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(aop, a, axes), f"f64 arg {op}")
+        want_cnt = (a == np.expand_dims(want, axes)).sum(axis=axes).astype(np.int32)
+        assert_bitexact(host(nt.Tensor._new_contiguous(cnt, kshape)), want_cnt, f"f64 count {op}")
