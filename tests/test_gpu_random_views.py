@@ -1,0 +1,138 @@
+"""Seeded random cases through the elementwise engine and the reductions:
+operand layouts drawn from contiguous, `.T`, broadcast row, broadcast
+column, scalar, every-other-column slice and one-element-offset views, on
+shapes with and without 4-aligned sides, so that every launch path (flat,
+rows, the tile kernels in each tile shape and orientation, generic) is
+crossed with the others and with partial tiles.  Each result is compared
+with the oracle on the same logical arrays: bit-exact for + - * / and the
+exact unary ops, the backward kernels' accumulation and max/min/argmax;
+sums within 1e-5 * sum|x|.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import assert_bitexact, assert_rel, dev, dev_T, host, rng
+
+import nanotorch_amd as nt
+from nanotorch_amd import _kernels as K
+from nanotorch_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+KINDS = ["contig", "T", "row", "col", "scalar", "slice", "offset"]
+SIDES = [1, 3, 4, 7, 16, 60, 64, 65, 100, 128, 132, 200, 257]
+
+
+def _values(r, shape, positive=False):
+    v = r.standard_normal(shape).astype(np.float32)
+    if positive:
+        v = (np.abs(v) + 0.5).astype(np.float32)
+    return v
+
+
+def _operand(r, shape, kind, positive=False):
+    """(device view, logical numpy array) of `shape` laid out as `kind`."""
+    R, C = shape
+    if kind == "T":
+        a = _values(r, shape, positive)
+        return dev_T(a), a
+    if kind == "row":
+        row = _values(r, (C,), positive)
+        return dev(row).expand(R, C), np.ascontiguousarray(np.broadcast_to(row, shape))
+    if kind == "col":
+        col = _values(r, (R, 1), positive)
+        return dev(col).expand(R, C), np.ascontiguousarray(np.broadcast_to(col, shape))
+    if kind == "scalar":
+        s = _values(r, (1, 1), positive)
+        return dev(s).expand(R, C), np.ascontiguousarray(np.broadcast_to(s, shape))
+    if kind == "slice":
+        big = _values(r, (R, 2 * C), positive)
+        return dev(big)[:, ::2], np.ascontiguousarray(big[:, ::2])
+    if kind == "offset":
+        flat = _values(r, (R * C + 1,), positive)
+        return dev(flat)[1:].reshape(R, C), flat[1:].reshape(R, C)
+    a = _values(r, shape, positive)
+    return dev(a), a
+
+
+def _target(r, shape, kind):
+    """A writable gradient target: contiguous or a `.T` view."""
+    a = _values(r, shape)
+    return (dev_T(a) if kind == "T" else dev(a)), a
+
+
+@pytest.mark.parametrize("case", range(60))
+def test_random_binary_and_unary(gpu, case):
+    r = rng(1000 + case)
+    shape = (int(r.choice(SIDES)), int(r.choice(SIDES)))
+    ka, kb = str(r.choice(KINDS)), str(r.choice(KINDS))
+    xa, a = _operand(r, shape, ka)
+    for op, oop in ((_lib.ADD, O.ADD), (_lib.SUB, O.SUB), (_lib.MUL, O.MUL), (_lib.DIV, O.DIV)):
+        xb, b = _operand(r, shape, kb, positive=(op == _lib.DIV))
+        got = host(nt.Tensor._new_contiguous(K.binary(op, xa, xb), shape))
+        assert_bitexact(got, O.binary(oop, a, b), f"case {case} op {op} {ka}/{kb} {shape}")
+    for op, oop in ((_lib.NEG, O.NEG), (_lib.RELU, O.RELU)):
+        got = host(nt.Tensor._new_contiguous(K.unary(op, xa, 0.0), shape))
+        assert_bitexact(got, O.unary(oop, a, 0.0), f"case {case} unary {op} {ka} {shape}")
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_random_fused_backward(gpu, case):
+    """mul backward into two gradient targets (contiguous or `.T`), and the
+    exp backward from a saved output, accumulating; operands of any
+    layout."""
+    r = rng(2000 + case)
+    shape = (int(r.choice(SIDES)), int(r.choice(SIDES)))
+    kg, ka, kb = (str(r.choice(KINDS)) for _ in range(3))
+    ta_kind, tb_kind = str(r.choice(["contig", "T"])), str(r.choice(["contig", "T"]))
+    xg, g = _operand(r, shape, kg)
+    xa, a = _operand(r, shape, ka)
+    xb, b = _operand(r, shape, kb)
+    tga, olda = _target(r, shape, ta_kind)
+    tgb, oldb = _target(r, shape, tb_kind)
+    K.binary_bwd(_lib.MUL, xg, xa, xb, True, tga, True, tgb)
+    wa, wb = O.bwd_binary(O.MUL, g, a, b)
+    tag = f"case {case} g={kg} a={ka} b={kb} ta={ta_kind} tb={tb_kind} {shape}"
+    assert_bitexact(host(tga), O.accumulate(olda, wa), "mul bwd a " + tag)
+    assert_bitexact(host(tgb), O.accumulate(oldb, wb), "mul bwd b " + tag)
+    y = O.unary(O.EXP, a, 0.0)
+    ky = str(r.choice(["contig", "T"]))
+    sy = dev_T(y) if ky == "T" else dev(y)
+    t, old = _target(r, shape, str(r.choice(["contig", "T"])))
+    K.unary_bwd(_lib.EXP, xg, sy, 0.0, t)
+    assert_bitexact(host(t), O.accumulate(old, O.bwd_exp(g, y)), "exp bwd " + tag)
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_random_reductions(gpu, case):
+    """sum / max / argmax over random axis sets of 2-D and 3-D contiguous,
+    transposed and sliced views."""
+    r = rng(3000 + case)
+    nd = int(r.choice([2, 3]))
+    sizes = [1, 2, 5, 31, 64, 100, 257, 1030, 4100] if nd == 2 else [1, 2, 5, 31, 64, 100, 257]
+    shape = tuple(int(r.choice(sizes)) for _ in range(nd))
+    base = r.integers(-50, 51, shape).astype(np.float32)
+    kind = str(r.choice(["contig", "T", "slice"]))
+    if kind == "T":
+        x = dev(np.ascontiguousarray(np.swapaxes(base, 0, -1))).transpose(0, nd - 1)
+        a = base
+    elif kind == "slice":
+        big = np.repeat(base, 2, axis=-1)
+        x, a = dev(big)[..., ::2], big[..., ::2]
+    else:
+        x, a = dev(base), base
+    naxes = int(r.integers(1, nd + 1))
+    axes = tuple(int(v) for v in r.permutation(nd)[:naxes])
+    kshape = tuple(s for i, s in enumerate(shape) if i not in axes)
+    tag = f"case {case} {shape} {kind} axes={axes}"
+    got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, axes, nt.float32), kshape))
+    want = O.reduce(O.R_SUM, a, axes, np.float32)
+    scale = O.reduce(O.R_SUM, np.abs(a).astype(np.float64), axes, np.float64)
+    assert_rel(got, want, 1e-5, "sum " + tag, scale=scale)
+    v, idx, cnt = K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True)
+    assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), O.reduce(O.R_MAX, a, axes), "max " + tag)
+    assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(O.R_ARGMAX, a, axes), "argmax " + tag)
