@@ -1,4 +1,5 @@
-"""Seeded random cases through the elementwise engine and the reductions:
+"""Seeded random cases through the elementwise engine, the reductions and
+matmul:
 operand layouts drawn from contiguous, `.T`, broadcast row, broadcast
 column, scalar, every-other-column slice and one-element-offset views, on
 shapes with and without 4-aligned sides, so that every launch path (flat,
@@ -136,3 +137,46 @@ def test_random_reductions(gpu, case):
     v, idx, cnt = K.reduce(_lib.R_MAX, x, axes, nt.float32, want_aux=True)
     assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), O.reduce(O.R_MAX, a, axes), "max " + tag)
     assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(O.R_ARGMAX, a, axes), "argmax " + tag)
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_random_matmul(gpu, case):
+    """Products of random sizes (ragged, multiples of 4, of 32 and of 256, so
+    that every matmul kernel and split-K are chosen), each operand
+    contiguous, transposed or a column slice, an optional batch, written
+    fresh or accumulated into a contiguous or `.T` target; within
+    1e-4 * (|A|.|B|)_ij of the oracle's sequential product."""
+    r = rng(4000 + case)
+    dims = [1, 3, 4, 32, 96, 100, 256, 260, 512, 1024]
+    M, Kd, N = (int(r.choice(dims)) for _ in range(3))
+    if M * N * Kd > 1024 * 1024 * 256:
+        Kd = 64
+    batch = int(r.choice([1, 1, 3]))
+    a = r.standard_normal((batch, M, Kd)).astype(np.float32)
+    b = (r.standard_normal((batch, Kd, N)) / np.sqrt(Kd)).astype(np.float32)
+
+    def place(v, kind):
+        if kind == "T":
+            return dev(np.ascontiguousarray(np.swapaxes(v, 1, 2))).transpose(1, 2)
+        if kind == "slice":
+            big = np.repeat(v, 2, axis=2)
+            return dev(big)[:, :, ::2]
+        return dev(v)
+
+    ka, kb = str(r.choice(["contig", "T", "slice"])), str(r.choice(["contig", "T", "slice"]))
+    xa, xb = place(a, ka), place(b, kb)
+    want = np.stack([O.matmul(a[i], b[i], parallel=True) for i in range(batch)])
+    scale = np.stack([O.matmul(np.abs(a[i]).astype(np.float64), np.abs(b[i]).astype(np.float64),
+                               parallel=True) for i in range(batch)])
+    tag = f"case {case} {batch}x{M}x{Kd}x{N} a={ka} b={kb}"
+    if r.random() < 0.5:
+        out_shape = (batch, M, N)
+        got = host(nt.Tensor._new_contiguous(K.matmul(xa, xb, out_shape), out_shape))
+        assert_rel(got, want, 1e-4, "fresh " + tag, scale=scale)
+    else:
+        old = r.standard_normal((batch, M, N)).astype(np.float32)
+        kt = str(r.choice(["contig", "T"]))
+        tgt = place(old, kt) if kt == "T" else dev(old)
+        K.matmul_into(xa, xb, tgt, accumulate=True)
+        assert_rel(host(tgt), want + old, 1e-4, f"accumulate into {kt} " + tag,
+                   scale=scale + np.abs(old))
