@@ -1,7 +1,7 @@
 """Seeded random cases through the elementwise engine, the reductions and
-matmul:
-operand layouts drawn from contiguous, `.T`, broadcast row, broadcast
-column, scalar, every-other-column slice and one-element-offset views, on
+matmul: operand layouts drawn from contiguous, `.T`, broadcast row,
+broadcast column, scalar, every-other-column slice and one-element-offset
+views, on
 shapes with and without 4-aligned sides, so that every launch path (flat,
 rows, the tile kernels in each tile shape and orientation, generic) is
 crossed with the others and with partial tiles.  Each result is compared
