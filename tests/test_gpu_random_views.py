@@ -1,13 +1,13 @@
 """Seeded random cases through the elementwise engine, the reductions and
 matmul: operand layouts drawn from contiguous, `.T`, broadcast row,
 broadcast column, scalar, every-other-column slice and one-element-offset
-views, on
-shapes with and without 4-aligned sides, so that every launch path (flat,
-rows, the tile kernels in each tile shape and orientation, generic) is
-crossed with the others and with partial tiles.  Each result is compared
-with the oracle on the same logical arrays: bit-exact for + - * / and the
-exact unary ops, the backward kernels' accumulation and max/min/argmax;
-sums within 1e-5 * sum|x|.
+views, on shapes with and without 4-aligned sides, so that every launch
+path (flat, rows, the tile kernels in each tile shape and orientation,
+generic; every matmul kernel and split-K) is crossed with the others and
+with partial tiles.  Each result is compared with the oracle on the same
+logical arrays: bit-exact for + - * / and the exact unary ops, the backward
+kernels' accumulation and max/min/argmax; sums within 1e-5 * sum|x|;
+products within 1e-4 * (|A|.|B|)_ij.
 """
 
 from __future__ import annotations
