@@ -461,7 +461,8 @@ def _index_args(fn: str, plan, first, second, keep_alive: list) -> list:
 def bench_next(iters: int = 12) -> dict:
     """The rows next to the hot path, each timed per launch with HIP events
     on the library stream: device casts and a comparison (no host round
-    trip), strided copy of a transposed view, a batched matmul on the MFMA
+    trip), strided copies of a transposed 2-D view and of a batch of
+    transposed planes, a batched matmul on the MFMA
     kernel, and advanced-index gather / scatter of rows.  Bytes are
     algorithmic (every operand once); GB/s against the HBM peak, TFLOP/s
     against the fp32 MFMA peak."""
@@ -507,6 +508,8 @@ def bench_next(iters: int = 12) -> dict:
     keep.append(vws)
     cmp_args = [(_lib.GT, ctypes.byref(x), ctypes.byref(y), ctypes.byref(z)) for x, y, z in vws]
     gbytes = 2 * gouts[0].numel * 4 + 8 * len(ids)
+    a3 = [t.reshape(64, 1024, 1024) for t in a]
+    o3 = [t.reshape(64, 1024, 1024) for t in o32]
     cases = {
         # name: (launch of set k, bytes or None, flop or None)
         "cast|f32->f64": (lambda k: K.copy_view(a[k], o64[k]), 12 * n, None),
@@ -514,6 +517,8 @@ def bench_next(iters: int = 12) -> dict:
         "cast|i64->f32": (lambda k: K.copy_view(lab[k], o32[k]), 12 * n, None),
         "compare|gt": (lambda k: _lib.call("nt_binary", *cmp_args[k]), 9 * n, None),
         "copy|transposed": (lambda k: K.copy_view(a[k].T, o32[k]), 8 * n, None),
+        # a batch of 64 planes: [64, 1024, 1024].transpose(1, 2) -> contiguous
+        "copy|3-D transpose(1,2)": (lambda k: K.copy_view(a3[k].transpose(1, 2), o3[k]), 8 * n, None),
         "matmul|batched 16x1024^3": (lambda k: K.matmul_into(xb, yb, ob3, accumulate=False),
                                      None, 2 * B * Mb**3),
         "gather|8192 rows of [50000,1024]": (lambda k: _lib.call("nt_gather_axes", *gargs[k]),

@@ -82,6 +82,13 @@ template <int N> struct Strides2 {
   int64_t c[N > 0 ? N : 1];
 };
 
+// Element offsets between consecutive batch elements of each operand (the
+// tile kernel over a batch of 2-D planes).
+template <int NI, int NO> struct BatchStrides {
+  int64_t in[NI > 0 ? NI : 1];
+  int64_t out[NO];
+};
+
 template <int N> struct StridesN {
   int64_t s[N][NT_MAX_DIMS];
 };
@@ -325,7 +332,7 @@ __global__ __launch_bounds__(TR * TC / 16) void ew_tile4_kernel(
     PtrPack<const TI, NI> in, Strides2<NI> sin, uint32_t row_in,
     uint32_t col_in, uint32_t bcol_in, PtrPack<TO, NO> out, Strides2<NO> sout,
     uint32_t row_out, uint32_t col_out, int64_t R, int64_t C, int64_t tiles_c,
-    F f) {
+    FastDivU32 tiles_b, BatchStrides<NI, NO> bs, F f) {
   // NTH work-items, each owning EL = 4 vectors of 4 elements per operand.
   // ROW ownership: vector f = t + NTH * i is row l = f / QC, columns
   // 4 * (f % QC) + 0..3; COL ownership: column f / QR, rows
@@ -335,8 +342,18 @@ __global__ __launch_bounds__(TR * TC / 16) void ew_tile4_kernel(
   constexpr size_t LB = sizeof(TI) > sizeof(TO) ? sizeof(TI) : sizeof(TO);
   __shared__ __align__(16) unsigned char lds_raw[EW_TILE_BUFS][TC * PR * LB];
   const int t = threadIdx.x;
+  // Workgroup b takes tile b % tiles_b of batch element b / tiles_b (one
+  // element, tiles_b = every tile, for a 2-D launch).
+  const uint32_t bb = tiles_b.div(blockIdx.x);
+  const uint32_t bt = blockIdx.x - bb * tiles_b.d;
+#pragma unroll
+  for (int k = 0; k < NI; ++k)
+    in.p[k] += int64_t(bb) * bs.in[k];
+#pragma unroll
+  for (int m = 0; m < NO; ++m)
+    out.p[m] += int64_t(bb) * bs.out[m];
   int64_t tr, tc;
-  diagonal_tile(blockIdx.x, (R + TR - 1) / TR, tiles_c, tr, tc);
+  diagonal_tile(bt, (R + TR - 1) / TR, tiles_c, tr, tc);
   const int64_t r0 = tr * TR, c0 = tc * TC;
 
   TI v[NI > 0 ? NI : 1][EL][4];
@@ -790,8 +807,12 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
     }
   }
 
-  // ---- tile2d
-  if (L.ndim == 2) {
+  // ---- tile2d: a 2-D iteration space, or a batch of 2-D planes (3-D after
+  // coalescing, e.g. `x.transpose(1, 2)` of a [B, M, N] tensor).  st holds
+  // each operand's (row, column) strides in the plane, bst its stride
+  // between batch elements (nb of them).
+  auto tile2d = [&](int64_t R0, int64_t C0, std::array<std::array<int64_t, 2>, NT> st,
+                    int64_t nb, const std::array<int64_t, NT> &bst) -> bool {
     // Elements are independent, so the tile may walk the transposed index
     // space.  Column-major operands go through the LDS exchange; pick the
     // orientation in which that costs less, an exchanged output counting
@@ -802,7 +823,7 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
     constexpr int OUT_COST = 3;
     int cost_keep = 0, cost_swap = 0;
     for (int k = 0; k < NT; ++k) {
-      const int64_t sr = L.strides[k][0], sc = L.strides[k][1];
+      const int64_t sr = st[k][0], sc = st[k][1];
       const int wgt = k < NI ? 1 : OUT_COST;
       if (sc == 1 && sr != 0) // row-major now, exchanged after a swap
         cost_swap += wgt;
@@ -810,16 +831,21 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
         cost_keep += wgt;
     }
     if (cost_swap < cost_keep) {
-      std::swap(L.shape[0], L.shape[1]);
+      std::swap(R0, C0);
       for (int k = 0; k < NT; ++k)
-        std::swap(L.strides[k][0], L.strides[k][1]);
+        std::swap(st[k][0], st[k][1]);
     }
     Strides2<NI> sin{};
     Strides2<NO> sout{};
+    BatchStrides<NI, NO> bs{};
     uint32_t col_in = 0, col_out = 0, row_in = 0, row_out = 0, bcol_in = 0;
-    const int64_t R = L.shape[0], C = L.shape[1];
-    // Vector path: 4-element groups stay inside the matrix and aligned.
+    const int64_t R = R0, C = C0;
+    // Vector path: 4-element groups stay inside the matrix and aligned (in
+    // every batch element).
     bool vec4 = R % 4 == 0 && C % 4 == 0 && sizeof(TI) <= 8 && sizeof(TO) <= 8;
+    for (int k = 0; k < NT; ++k)
+      if (bst[k] % 4 != 0)
+        vec4 = false;
     auto classify = [&](int64_t sr, int64_t sc, const void *p, size_t es,
                         uint32_t bit, uint32_t &row, uint32_t &col) {
       const bool al = reinterpret_cast<uintptr_t>(p) % (4 * es) == 0;
@@ -834,35 +860,38 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       }
     };
     for (int k = 0; k < NI; ++k) {
-      sin.r[k] = L.strides[k][0];
-      sin.c[k] = L.strides[k][1];
+      sin.r[k] = st[k][0];
+      sin.c[k] = st[k][1];
+      bs.in[k] = bst[k];
       classify(sin.r[k], sin.c[k], pin.p[k], sizeof(TI), 1u << k, row_in, col_in);
       if (sin.c[k] == 0 && sin.r[k] != 0)
         bcol_in |= 1u << k;
     }
     for (int m = 0; m < NO; ++m) {
-      sout.r[m] = L.strides[NI + m][0];
-      sout.c[m] = L.strides[NI + m][1];
+      sout.r[m] = st[NI + m][0];
+      sout.c[m] = st[NI + m][1];
+      bs.out[m] = bst[NI + m];
       classify(sout.r[m], sout.c[m], pout.p[m], sizeof(TO), 1u << m, row_out, col_out);
     }
     // 16-byte tile kernel: TR x TC tiles, TR * TC / 16 work-items.
     auto tile4 = [&]<int TR, int TC>() {
       constexpr int64_t NTH = TR * TC / 16;
       const int64_t tr_n = (R + TR - 1) / TR, tc_n = (C + TC - 1) / TC;
-      const int64_t blocks = tr_n * tc_n;
+      const int64_t blocks = tr_n * tc_n * nb;
       if (blocks * NTH >= (int64_t(1) << 32))
         return false;
       const dim3 grid{unsigned(blocks), 1u, 1u};
+      const FastDivU32 tb(uint32_t(tr_n * tc_n));
       if (ntl)
         ew_tile4_kernel<TI, TO, NI, NO, true, TR, TC, F>
             <<<grid, unsigned(NTH), 0, s>>>(pin, sin, row_in, col_in, bcol_in,
                                             pout, sout, row_out, col_out, R, C,
-                                            tc_n, f);
+                                            tc_n, tb, bs, f);
       else
         ew_tile4_kernel<TI, TO, NI, NO, false, TR, TC, F>
             <<<grid, unsigned(NTH), 0, s>>>(pin, sin, row_in, col_in, bcol_in,
                                             pout, sout, row_out, col_out, R, C,
-                                            tc_n, f);
+                                            tc_n, tb, bs, f);
       NT_LAUNCH_CHECK();
       return true;
     };
@@ -878,31 +907,57 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       // streams (binary forwards, unary backwards) were best at 64 x 64
       // (the whole sweep 0.2 / 0.7 / 2.3% slower with 64 x 128, 128 x 64 or
       // 128 x 128 for them).  Whole sweep +0.8%.
-      bool done = false;
       if constexpr (std::is_same_v<TI, float> && std::is_same_v<TO, float>) {
         const int n_col = __builtin_popcount(col_in) + __builtin_popcount(col_out);
         const int n_row = __builtin_popcount(row_in) + __builtin_popcount(row_out);
         if (n_col == 1 && n_row >= 3)
-          done = tile4.template operator()<128, 64>();
-        else if (n_col == 1)
-          done = tile4.template operator()<64, 128>();
-        else
-          done = tile4.template operator()<64, 64>();
+          return tile4.template operator()<128, 64>();
+        if (n_col == 1)
+          return tile4.template operator()<64, 128>();
+        return tile4.template operator()<64, 64>();
       } else {
-        done = tile4.template operator()<64, 64>();
+        return tile4.template operator()<64, 64>();
       }
-      if (done)
-        return;
     }
+    // element tiles: one plane only
     const int64_t tiles_r = (R + EW_TILE - 1) / EW_TILE;
     const int64_t tiles_c = (C + EW_TILE - 1) / EW_TILE;
     const int64_t blocks = tiles_r * tiles_c;
-    if (!vec4 && blocks * EW_THREADS < (int64_t(1) << 32)) {
+    if (nb == 1 && blocks * EW_THREADS < (int64_t(1) << 32)) {
       const dim3 grid{unsigned(blocks), 1u, 1u};
       ew_tile_kernel<TI, TO, NI, NO, F><<<grid, EW_THREADS, 0, s>>>(
           pin, sin, col_in, pout, sout, col_out, R, C, tiles_c, f);
       NT_LAUNCH_CHECK();
+      return true;
+    }
+    return false;
+  };
+  if (L.ndim == 2) {
+    std::array<std::array<int64_t, 2>, NT> st{};
+    std::array<int64_t, NT> bst{};
+    for (int k = 0; k < NT; ++k)
+      st[k] = {L.strides[k][0], L.strides[k][1]};
+    if (tile2d(L.shape[0], L.shape[1], st, 1, bst))
       return;
+  } else if (L.ndim == 3) {
+    // The batch axis is the one on which no operand has unit stride; the
+    // other two (in order) form the plane.
+    for (int z = 0; z < 3; ++z) {
+      bool unit = false;
+      for (int k = 0; k < NT; ++k)
+        unit = unit || L.strides[k][z] == 1;
+      if (unit)
+        continue;
+      const int pa = z == 0 ? 1 : 0, pb = z == 2 ? 1 : 2;
+      std::array<std::array<int64_t, 2>, NT> st{};
+      std::array<int64_t, NT> bst{};
+      for (int k = 0; k < NT; ++k) {
+        st[k] = {L.strides[k][pa], L.strides[k][pb]};
+        bst[k] = L.strides[k][z];
+      }
+      if (tile2d(L.shape[pa], L.shape[pb], st, L.shape[z], bst))
+        return;
+      break;
     }
   }
 

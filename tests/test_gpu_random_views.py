@@ -180,3 +180,54 @@ def test_random_matmul(gpu, case):
         K.matmul_into(xa, xb, tgt, accumulate=True)
         assert_rel(host(tgt), want + old, 1e-4, f"accumulate into {kt} " + tag,
                    scale=scale + np.abs(old))
+
+
+PERMS = [(0, 2, 1), (2, 1, 0), (1, 0, 2), (1, 2, 0), (2, 0, 1)]
+
+
+def _permute(t, perm):
+    """The view of t whose axis i is t's axis perm[i], by transposes."""
+    cur = list(range(len(perm)))
+    for i, want in enumerate(perm):
+        j = cur.index(want)
+        if j != i:
+            t = t.transpose(i, j)
+            cur[i], cur[j] = cur[j], cur[i]
+    return t
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_random_3d_permutes(gpu, case):
+    """Copies, binary ops and the mul backward on permuted 3-D views (a
+    batch of 2-D planes for the tile kernel when the unit strides share a
+    plane, the generic kernel otherwise), against numpy's transpose."""
+    r = rng(5000 + case)
+    sides = [1, 3, 4, 8, 12, 64, 65, 128, 132]
+    base_shape = tuple(int(r.choice(sides)) for _ in range(3))
+    pa, pb = PERMS[int(r.integers(len(PERMS)))], PERMS[int(r.integers(len(PERMS)))]
+    a0 = r.standard_normal(base_shape).astype(np.float32)
+    xa = _permute(dev(a0), pa)
+    a = np.ascontiguousarray(a0.transpose(pa))
+    shape = a.shape
+    # b: stored so that its permutation pb gives the logical shape of a
+    inv = np.argsort(pb)
+    b0 = r.standard_normal(tuple(shape[i] for i in inv)).astype(np.float32)
+    xb = _permute(dev(b0), pb)
+    b = np.ascontiguousarray(b0.transpose(pb))
+    assert b.shape == shape
+    tag = f"case {case} base {base_shape} perms {pa} {pb}"
+    out = dev(np.zeros(shape, np.float32))
+    K.copy_view(xa, out)
+    assert_bitexact(host(out), a, "copy " + tag)
+    for op, oop in ((_lib.ADD, O.ADD), (_lib.MUL, O.MUL)):
+        got = host(nt.Tensor._new_contiguous(K.binary(op, xa, xb), shape))
+        assert_bitexact(got, O.binary(oop, a, b), f"op {op} " + tag)
+    g = r.standard_normal(shape).astype(np.float32)
+    olds = [r.standard_normal(shape).astype(np.float32) for _ in range(2)]
+    # gradient targets laid out like the operands
+    ta = _permute(dev(np.ascontiguousarray(olds[0].transpose(np.argsort(pa)))), pa)
+    tb = dev(olds[1])
+    K.binary_bwd(_lib.MUL, dev(g), xa, xb, True, ta, True, tb)
+    wa, wb = O.bwd_binary(O.MUL, g, a, b)
+    assert_bitexact(host(ta), O.accumulate(olds[0], wa), "mul bwd a " + tag)
+    assert_bitexact(host(tb), O.accumulate(olds[1], wb), "mul bwd b " + tag)
