@@ -881,7 +881,7 @@ PROFILE_FILES = {
     "red": ("reduce_config3_trace.md", "Kernel statistics: config-3 reductions [8192, 8192] fp32"),
     "mm": ("matmul_config4_trace.md", "Kernel statistics: config-4 MatMulOp forward + dA + dB"),
     "mlp": ("mlp_config5_trace.md", "Kernel statistics: config-5 4-layer MLP training steps"),
-    "next": ("next_rows_trace.md", "Kernel statistics: casts, comparison, strided copy, device uniform draws, "
+    "next": ("next_rows_trace.md", "Kernel statistics: casts, comparison, strided copies (2-D and batched 3-D transposes, one tile kernel), device uniform draws, "
                                    "batched matmul, gather / scatter (the rows beside the path)"),
 }
 _UN = {0: "exp", 1: "log", 2: "neg", 3: "relu", 4: "sqrt", 5: "tanh", 6: "sigmoid", 7: "pow"}
