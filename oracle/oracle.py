@@ -23,7 +23,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "libnt_oracle.so")
+# NT_ORACLE_LIB selects another build of the same source (the sanitizer
+# build of tests/test_oracle_sanitized.py).
+LIB = os.environ.get("NT_ORACLE_LIB") or os.path.join(HERE, "libnt_oracle.so")
 
 EXP, LOG, NEG, RELU, SQRT, TANH, SIGMOID, POW = range(8)
 ADD, SUB, MUL, DIV, EQ, GT, GE = range(7)
