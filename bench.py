@@ -630,16 +630,20 @@ def _timed(fn) -> float:
     return time.perf_counter() - t0
 
 
-def cpu_per_op(rows: int = 512) -> dict:
+def cpu_per_op(rows: int = 4096) -> dict:
     """ref-cpu-1t: the oracle (the reference's CPU kernels and Python
     backward compositions, restated; single thread, as the reference has no
     threads) timed per op on bounded samples of configs 2-5, with the GPU
     figures' byte / FLOP models, so that every GPU per-kernel figure has a
     CPU figure beside it.
 
-    config 2: [rows, 4096] (rows/4096 of the workload), each op's forward and
-      its backward composition plus the engine's accumulate, both layouts
-      (the transposed sample is the .T view of a contiguous [4096, rows]);
+    config 2: [rows, 4096] (by default the whole [4096, 4096] workload,
+      10-40 s single-threaded depending on the host; a smaller sample would
+      sit in the host caches and overstate the CPU rate), each op's forward and its backward
+      composition plus the engine's accumulate, both layouts (the transposed
+      operands are .T views of contiguous [4096, rows] arrays); the inputs
+      of every op come from one pool per layout drawn from the op domains
+      (arrays far larger than the host caches, so reuse warms nothing);
     config 3: [512, 8192] (1/16 of the rows), sum / max / min forward and
       sum (accumulate) / mean / max backward along axis 0, axis 1 and all;
     config 4: 2 output rows of each product (fwd, dA = dG.B^T, dB = A^T.dG,
@@ -660,11 +664,17 @@ def cpu_per_op(rows: int = 512) -> dict:
     tot_b = tot_s = 0.0
     for layout in ("contig", "transposed"):
         mk = (lambda a: a) if layout == "contig" else (lambda a: np.ascontiguousarray(a.T).T)
+
+        def draw(dom):
+            v = r.standard_normal(shape) if dom is None else r.uniform(dom[0], dom[1], shape)
+            return mk(v.astype(np.float32))
+        pool = {dom: draw(dom) for dom in (None, (0.5, 2), (0.1, 4), (-4, 4))}
+        pool["b"] = draw(None)
+        g = r.standard_normal(shape).astype(np.float32)
+        olds = [draw(None) for _ in range(2)]
         for name, op in (("add", O.ADD), ("sub", O.SUB), ("mul", O.MUL), ("truediv", O.DIV)):
-            a = mk(r.standard_normal(shape).astype(np.float32))
-            b = mk((r.uniform(0.5, 2, shape) if name == "truediv" else r.standard_normal(shape)).astype(np.float32))
-            g = r.standard_normal(shape).astype(np.float32)
-            olds = [mk(r.standard_normal(shape).astype(np.float32)) for _ in range(2)]
+            a = pool[None]
+            b = pool[(0.5, 2)] if name == "truediv" else pool["b"]
             tf = _timed(lambda: O.binary(op, a, b))
 
             def bwd():
@@ -678,9 +688,8 @@ def cpu_per_op(rows: int = 512) -> dict:
                 tot_b += nb
                 tot_s += t
         for name, op, dom, saved, e in UNARY_OPS:
-            x = mk((r.standard_normal(shape) if dom is None else r.uniform(dom[0], dom[1], shape)).astype(np.float32))
-            g = r.standard_normal(shape).astype(np.float32)
-            old = mk(r.standard_normal(shape).astype(np.float32))
+            x = pool[dom]
+            old = olds[0]
             oop = {"neg": O.NEG, "exp": O.EXP, "log": O.LOG, "sqrt": O.SQRT, "pow": O.POW,
                    "relu": O.RELU, "sigmoid": O.SIGMOID, "tanh": O.TANH}[name]
             y = None
@@ -699,9 +708,10 @@ def cpu_per_op(rows: int = 512) -> dict:
                 out["elementwise"][f"{name}|{layout}|{phase}"] = round(nb / t / 1e9, 3)
                 tot_b += nb
                 tot_s += t
-    out["elementwise_sample"] = f"[{rows}, 4096] (1/{4096 // rows} of config 2)"
+    part = "the whole config-2 workload" if rows == 4096 else f"1/{4096 // rows} of config 2"
+    out["elementwise_sample"] = f"[{rows}, 4096] ({part})"
     baseline = {"value": round(tot_b / tot_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"config-2 sweep on [{rows},4096] (1/{4096 // rows} of the workload), "
+                "sample": f"config-2 sweep on [{rows},4096] ({part}), "
                           f"forward + reference backward composition + accumulate, both layouts, "
                           f"single thread, {tot_s:.1f} s",
                 "host_cpu": _host_cpu(), "host_nproc": os.cpu_count()}
@@ -817,7 +827,7 @@ def cpu_parts() -> dict:
             dt_s = time.perf_counter() - t0
             red[f"{name}|{label}|fwd"] = round(x.nbytes / dt_s / 1e9, 3)
     out["reductions_GB/s_1thread"] = red
-    out["reductions_sample"] = "[512, 8192] fp32 (1/16 of config 3)"
+    out["reductions_sample"] = "[1024, 8192] fp32 (1/8 of config 3)"
     # config 4 sample: 512^3 single thread, 1024^3 on all cores
     mm = {}
     for n, par in ((512, False), (1024, True)):
