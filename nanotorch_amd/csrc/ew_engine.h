@@ -127,10 +127,51 @@ __device__ __forceinline__ VecT<T, VEC> vload(const T *p) {
   }
 }
 
-template <bool NTS, class T, int VEC>
+// Store forms.  ST_STREAM carries the nontemporal hint (global_store ... nt).
+// ST_THROUGH is a device-scope store (buffer_store ... sc1): it writes
+// through the XCD's L2 instead of leaving the line dirty there.  A kernel
+// with one output stream runs faster that way on MI355X: on cold 64 MB
+// arrays, back-to-back launches, y = -x 21.9 -> 20.3 us, y = a * b 31.7 ->
+// 29.4 us, gx += g * y 43.0 -> 37.8 us, the 64x64 transposed tile of
+// y = -x.T 24.9 -> 21.4 us; with two output streams (the binary backwards)
+// it measured no faster and up to 4% slower than ST_STREAM.  The compiler
+// emits the scope bit only on buffer stores (the buffer-store builtin's
+// cache-policy argument), so ST_THROUGH stores go through vstore_through
+// with a wave-uniform base; 64-bit atomic stores at device scope carry the
+// bit too but measured 50% slower (two 8-byte stores per 16 bytes).
+enum : int { ST_PLAIN = 0, ST_STREAM = 1, ST_THROUGH = 2 };
+
+// Which one-output kernels store through, by kernel kind.  Kernels queued
+// back to back share the cost of the streaming stores' dirty L2 lines: a
+// kernel that leaves them makes the next one slower while they drain, so
+// per-kernel times move between neighbours and the totals decide.  With the
+// flat kernels, the transposed tiles and the max/min backward over all axes
+// storing through, against every store streaming (one MI355X, two rounds per
+// build): config-2 sweep 5780-5788 -> 5848-5857 GB/s (+1.2%; per kernel the
+// accumulating backwards gain 8-13% and the transposed forwards lose 2-6%,
+// as each kernel now pays for its own writes), config-3 reductions
+// 6374-6387 -> 6466-6476 GB/s (+1.4%; the sum / mean / max backwards over
+// all axes +4-18%), config-5 step unchanged within its run-to-run spread.
+// The rows kernel (sum / mean backward along one axis, bias adds) and the
+// 2-D max/min backward storing through as well cost the reductions 1%
+// (axis-1 backwards -3 to -14%, axis 0 +7%): they keep streaming stores.
+enum : int { TK_FLAT = 1, TK_ROWS = 2, TK_TILE = 4, TK_SEL2D = 8, TK_SELVEC = 16 };
+constexpr bool through_pays(int kind) {
+  return kind == TK_FLAT || kind == TK_TILE || kind == TK_SELVEC;
+}
+
+// The form a kernel of kind KIND with NOUT output streams uses when
+// streaming is on.
+constexpr int store_form(bool stream, int nout, int kind) {
+  return !stream ? ST_PLAIN
+                 : ((nout == 1 && through_pays(kind)) ? ST_THROUGH : ST_STREAM);
+}
+
+// Plain or streaming store of one vector (ST_THROUGH is vstore_through's).
+template <int SF, class T, int VEC>
 __device__ __forceinline__ void vstore(T *p, const VecT<T, VEC> &w) {
   constexpr int BYTES = VEC * int(sizeof(T));
-  if constexpr (NTS && BYTES % 16 == 0) {
+  if constexpr (SF == ST_STREAM && BYTES % 16 == 0) {
     typedef int nat4 __attribute__((ext_vector_type(4)));
     nat4 v[BYTES / 16];
     __builtin_memcpy(v, &w, sizeof(v));
@@ -139,6 +180,79 @@ __device__ __forceinline__ void vstore(T *p, const VecT<T, VEC> &w) {
       __builtin_nontemporal_store(v[c], reinterpret_cast<nat4 *>(p) + c);
   } else {
     *reinterpret_cast<VecT<T, VEC> *>(p) = w;
+  }
+}
+
+// Buffer resources for vstore_through: a raw buffer (stride 0) of 2^31 - 1
+// bytes from the base; the fourth word's data format field (32-bit) must be
+// non-zero for untyped buffer accesses on CDNA.
+constexpr int BUF_WORD3 = 0x00020000;
+constexpr int BUF_BYTES = 0x7fffffff;
+constexpr int CPOL_SC1 = 16; // the cache-policy argument's device-scope bit
+
+// True when every byte a workgroup stores lies less than 2^31 bytes past the
+// base it passes to vstore_through (its largest element offset is last_off).
+template <class T>
+__device__ __forceinline__ bool through_fits(int64_t last_off, int vec) {
+  return (last_off + vec) * int64_t(sizeof(T)) <= int64_t(BUF_BYTES);
+}
+
+// Device-scope store of the VEC elements at base + off.  base must be the
+// same for every lane of the wave (it goes into the scalar buffer resource);
+// off * sizeof(T) + the vector's bytes must stay below 2^31 (through_fits).
+template <class T, int VEC>
+__device__ __forceinline__ void vstore_through(T *base, int64_t off,
+                                               const VecT<T, VEC> &w) {
+  constexpr int BYTES = VEC * int(sizeof(T));
+  // The callers' bases depend only on the workgroup (or the wave) and the
+  // kernel arguments, but the compiler does not always prove it (a tile's
+  // origin from its diagonal order was taken for divergent, which wrapped
+  // the store in a loop over distinct bases); reading the first active
+  // lane's copy states it.
+  const uint64_t ub = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(ub));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(ub >> 32));
+  T *const ubase = reinterpret_cast<T *>((uint64_t(hi) << 32) | lo);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(ubase, 0, BUF_BYTES, BUF_WORD3);
+  const int boff = int(off * int64_t(sizeof(T)));
+  if constexpr (BYTES % 16 == 0) {
+    typedef int nat4 __attribute__((ext_vector_type(4)));
+    nat4 v[BYTES / 16];
+    __builtin_memcpy(v, &w, sizeof(v));
+#pragma unroll
+    for (int c = 0; c < BYTES / 16; ++c)
+      __builtin_amdgcn_raw_buffer_store_b128(v[c], rs, boff + 16 * c, 0,
+                                             CPOL_SC1);
+  } else if constexpr (BYTES == 8) {
+    typedef int nat2 __attribute__((ext_vector_type(2)));
+    nat2 v;
+    __builtin_memcpy(&v, &w, sizeof(v));
+    __builtin_amdgcn_raw_buffer_store_b64(v, rs, boff, 0, CPOL_SC1);
+  } else if constexpr (BYTES == 4) {
+    int v;
+    __builtin_memcpy(&v, &w, sizeof(v));
+    __builtin_amdgcn_raw_buffer_store_b32(v, rs, boff, 0, CPOL_SC1);
+  } else {
+    *reinterpret_cast<VecT<T, VEC> *>(ubase + off) = w;
+  }
+}
+
+// The store of one output vector in a kernel with NO outputs: through the
+// workgroup's uniform base when that form applies and fits, else plain or
+// streaming at base + off.
+template <bool NTL, int NO, int KIND, class T, int VEC>
+__device__ __forceinline__ void vstore_out(T *base, int64_t off, bool fits,
+                                           const VecT<T, VEC> &w) {
+  constexpr int SF = store_form(NTL, NO, KIND);
+  if constexpr (SF == ST_THROUGH) {
+    if (fits) {
+      vstore_through<T, VEC>(base, off, w);
+      return;
+    }
+    vstore<ST_STREAM, T, VEC>(base + off, w);
+  } else {
+    vstore<SF, T, VEC>(base + off, w);
   }
 }
 
@@ -156,8 +270,10 @@ __global__ __launch_bounds__(FLAT_THREADS) void ew_flat_kernel(
     int64_t nvec, int64_t n, F f) {
   using VI = VecT<TI, VEC>;
   using VO = VecT<TO, VEC>;
-  const int64_t base =
-      int64_t(blockIdx.x) * (FLAT_THREADS * UNROLL) + threadIdx.x;
+  // wg0: the workgroup's first vector (its outputs start there: a uniform
+  // base for device-scope stores, offsets below FLAT_THREADS * UNROLL)
+  const int64_t wg0 = int64_t(blockIdx.x) * (FLAT_THREADS * UNROLL);
+  const int64_t base = wg0 + threadIdx.x;
   VI a[UNROLL][NI > 0 ? NI : 1];
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
@@ -195,7 +311,8 @@ __global__ __launch_bounds__(FLAT_THREADS) void ew_flat_kernel(
       }
 #pragma unroll
       for (int m = 0; m < NO; ++m)
-        vstore<NTL, TO, VEC>(out.p[m] + int64_t(vi) * VEC, o[m]);
+        vstore_out<NTL, NO, TK_FLAT, TO, VEC>(out.p[m] + wg0 * VEC, (vi - wg0) * VEC,
+                                     true, o[m]);
     }
   }
   // Fewer than VEC trailing elements: block 0 takes them one per thread.
@@ -234,6 +351,13 @@ __global__ __launch_bounds__(NT_ROWS_THREADS) void ew_rows_kernel(
   using VI = VecT<TI, VEC>;
   using VO = VecT<TO, VEC>;
   const uint32_t vi = blockIdx.x * NT_ROWS_THREADS + threadIdx.x;
+  // The workgroup's first and last row groups: its outputs lie in rows
+  // [rbase, rlast * RR + RR), a uniform base for device-scope stores.
+  const uint32_t v0 = blockIdx.x * NT_ROWS_THREADS;
+  const uint32_t vl = (v0 + NT_ROWS_THREADS < nvec ? v0 + NT_ROWS_THREADS : nvec) - 1;
+  const int64_t rbase = int64_t(fdc.div(v0 * VEC)) * RR;
+  const bool fits = through_fits<TO>(
+      (int64_t(fdc.div(vl * VEC)) * RR + RR - rbase) * C - 1, 1);
   if (vi >= nvec)
     return;
   const uint32_t i = vi * VEC;
@@ -288,7 +412,8 @@ __global__ __launch_bounds__(NT_ROWS_THREADS) void ew_rows_kernel(
     }
 #pragma unroll
     for (int m = 0; m < NO; ++m)
-      vstore<NTL, TO, VEC>(out.p[m] + r * C + c, o[m]);
+      vstore_out<NTL, NO, TK_ROWS, TO, VEC>(out.p[m] + rbase * C, (r - rbase) * C + c,
+                                   fits, o[m]);
   }
 }
 
@@ -452,6 +577,10 @@ __global__ __launch_bounds__(TR * TC / 16) void ew_tile4_kernel(
   for (int m = 0; m < NO; ++m) {
     TO *p = out.p[m];
     const int64_t sr = sout.r[m], sc = sout.c[m];
+    // the tile's first element: a uniform base for device-scope stores
+    TO *const tb = p + r0 * sr + c0 * sc;
+    const bool fits = sr >= 0 && sc >= 0 &&
+                      through_fits<TO>((TR - 1) * sr + (TC - 1) * sc, 1);
     if (col_out & (1u << m)) {
       if (EW_TILE_BUFS == 1 && rnd > 0)
         __syncthreads();
@@ -476,7 +605,7 @@ __global__ __launch_bounds__(TR * TC / 16) void ew_tile4_kernel(
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             w.v[j] = lds[ll * PR + 4 * qq + j];
-          vstore<NTL, TO, 4>(p + r + c * sc, w);
+          vstore_out<NTL, NO, TK_TILE, TO, 4>(tb, 4 * qq + ll * sc, fits, w);
         }
       }
     } else if (row_out & (1u << m)) {
@@ -490,7 +619,7 @@ __global__ __launch_bounds__(TR * TC / 16) void ew_tile4_kernel(
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             w.v[j] = o[m][i][j];
-          vstore<NTL, TO, 4>(p + r * sr + c, w);
+          vstore_out<NTL, NO, TK_TILE, TO, 4>(tb, l * sr + 4 * q, fits, w);
         }
       }
     } else {

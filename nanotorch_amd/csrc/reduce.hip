@@ -971,8 +971,11 @@ __global__ __launch_bounds__(256) void sel_bwd_vec_kernel(
     const int32_t *__restrict__ cnt, T *gx, FastDivU32 fdC, uint32_t C,
     int64_t n4) {
   const int64_t stride = int64_t(gridDim.x) * 256;
-  for (int64_t q = int64_t(blockIdx.x) * 256 + threadIdx.x; q < n4;
-       q += stride) {
+  // q0: the block's first vector this round (uniform: the store base)
+  for (int64_t q0 = int64_t(blockIdx.x) * 256; q0 < n4; q0 += stride) {
+    const int64_t q = q0 + threadIdx.x;
+    if (q >= n4)
+      break;
     VecT<T, 4> o;
     VecT<T, 4> old;
     if constexpr (ACC)
@@ -1001,7 +1004,8 @@ __global__ __launch_bounds__(256) void sel_bwd_vec_kernel(
       else
         o.v[e] = t;
     }
-    vstore<true, T, 4>(gx + 4 * q, o); // streaming store
+    vstore_out<true, 1, TK_SELVEC, T, 4>(gx + 4 * q0, 4 * int64_t(threadIdx.x),
+                                         true, o);
   }
 }
 
@@ -1016,13 +1020,18 @@ __global__ __launch_bounds__(256) void sel_bwd_2d_kernel(
     const T *__restrict__ g, const int64_t *__restrict__ idx,
     const int32_t *__restrict__ cnt, T *gx, int64_t Rr, int64_t Cc,
     int64_t rpb) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // w is the same for every lane of a wave; readfirstlane tells the
+  // compiler so, which keeps each row's store base below in scalar registers
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t c = (int64_t(blockIdx.x) * 64 + lane) * 4;
   const int64_t r0 = int64_t(blockIdx.y) * rpb;
   const int64_t r1 = r0 + rpb < Rr ? r0 + rpb : Rr;
   const bool live = c < Cc;
   auto put = [&](int64_t r, const T (&t)[4]) {
-    T *p = gx + r * Cc + c;
+    // row r from the block's first column: wave-uniform (r is)
+    T *const rb = gx + r * Cc + int64_t(blockIdx.x) * 256;
+    T *p = rb + 4 * lane;
     VecT<T, 4> o;
     if constexpr (ACC) {
       const VecT<T, 4> old = vload<true, T, 4>(p);
@@ -1034,9 +1043,9 @@ __global__ __launch_bounds__(256) void sel_bwd_2d_kernel(
       for (int e = 0; e < 4; ++e)
         o.v[e] = t[e];
     }
-    // streaming store (measured: 0.75-0.77 -> 0.80-0.81 of peak for the
-    // axis-0 and axis-1 max backward on [8192, 8192])
-    vstore<true, T, 4>(p, o);
+    // (streaming stores measured 0.75-0.77 -> 0.80-0.81 of peak against
+    // plain ones for the axis-0 and axis-1 max backward on [8192, 8192])
+    vstore_out<true, 1, TK_SEL2D, T, 4>(rb, 4 * lane, true, o);
   };
   if constexpr (MODE == 1) {
     // reduced axis leading: column c's g / idx / count, loaded once
