@@ -138,3 +138,25 @@ def test_fill_past_64_gib():
     assert at(x, 2**32 * 4 - 1) == 3.0
     assert at(x, n - 1) == 3.0
     assert at(x, n - 13) == 3.0
+
+
+@pytest.mark.parametrize("row_stride", [2**23, 2**24])
+def test_tile_store_far_apart_rows(row_stride):
+    # out[...] = x.T into the first 192 columns of a [256, row_stride] fp32
+    # buffer: the transposed tile kernel (64 x 128 tiles) writes rows
+    # row_stride elements apart.  With 2^23 a tile's rows span just under
+    # 2^31 bytes, the byte offsets of its device-scope buffer stores reach
+    # 2.11e9; with 2^24 they would pass 2^31, so the kernel takes the
+    # streaming-store path instead.  Columns past 192 must stay untouched.
+    import numpy as np
+    R, C = 256, 192
+    big = nt.zeros(R, row_stride, device="cuda")
+    out = big[:, :C]
+    xs = (np.arange(C * R, dtype=np.float32) % 1021.0).reshape(C, R)
+    x = nt.tensor(xs.tolist()).to("cuda")
+    out[...] = x.T
+    got = np.array(out.cpu().tolist(), dtype=np.float32)
+    assert np.array_equal(got, xs.T)
+    edge = np.array(big[:, C:C + 8].cpu().tolist(), dtype=np.float32)
+    assert not edge.any()
+    assert at(big, R - 1, row_stride - 1) == 0.0
