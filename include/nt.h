@@ -205,6 +205,17 @@ int nt_binary_bwd(int32_t op, const nt_view *g, const nt_view *a,
                   const nt_view *b, const nt_view *ga, int32_t acc_a,
                   const nt_view *gb, int32_t acc_b);
 
+/* Fused SGD update of one parameter, in place: p = p - (g * lr).  The
+ * reference has no such kernel: `GradientDescent.step` runs
+ * `p -= p.grad * lr` under no_grad (src/nanotorch/nn/optimizers.py:45-51),
+ * a multiply kernel into a temporary (binary_ops.cu:109) and then
+ * `sub_inplace` (src/cpp/ops/inplace_ops.cu:63-79).  This keeps both fp32
+ * roundings (the product, then the difference) in one pass and no
+ * temporary.  p and g share one shape and the float32 dtype; lr is the
+ * float32 value of the step size (the reference's 0-d scalar tensor).  The
+ * storage version bump stays with the caller. */
+int nt_sgd_step(const nt_view *p, const nt_view *g, double lr);
+
 /* ------------------------------------------------------------- reductions */
 
 /* Replaces `sum, min, max, argmin, argmax` (src/cpp/ops/reduction_ops.cu:

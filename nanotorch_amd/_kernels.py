@@ -90,6 +90,16 @@ def binary(op: int, x1, x2) -> Storage:
     return out
 
 
+def sgd_step(p, g, lr32: float) -> None:
+    """p = p - (g * lr32) in one pass, in place (the two roundings of the
+    reference's `p -= p.grad * lr`, nn/optimizers.py:45-51); float32
+    device tensors of one shape, lr32 already a float32 value."""
+    require_device(p, g)
+    vp, vg = view_of(p), view_of(g)
+    _lib.call("nt_sgd_step", ctypes.byref(vp), ctypes.byref(vg), lr32)
+    p._storage.bump_version()
+
+
 def inplace(op: int, out, other) -> None:
     """out = out (op) other, in place (reference: inplace_ops.cu:39-79)."""
     require_device(out, other)

@@ -72,6 +72,7 @@ _SIGNATURES = {
     "nt_inplace": (c_int, [c_int32, _VP, _VP]),
     "nt_equals": (c_int, [_VP, _VP, POINTER(c_int32)]),
     "nt_unary_bwd": (c_int, [c_int32, _VP, _VP, c_double, _VP, c_int32]),
+    "nt_sgd_step": (c_int, [_VP, _VP, c_double]),
     "nt_binary_bwd": (c_int, [c_int32, _VP, _VP, _VP, _VP, c_int32, _VP, c_int32]),
     "nt_reduce": (c_int, [c_int32, _VP, POINTER(c_int64), c_int32, _VP, _VP, _VP]),
     "nt_reduce_noalloc": (c_int, [c_int32, _VP, POINTER(c_int64), c_int32, _VP, _VP, _VP]),

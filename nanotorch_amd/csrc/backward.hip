@@ -201,6 +201,17 @@ void binary_bwd_t(const nt_view *g, const nt_view *a, const nt_view *b,
   }
 }
 
+// p - (g * lr): the multiply kernel's rounding, then sub_inplace's (no
+// contraction: the build passes -ffp-contract=off).
+struct SgdStep {
+  float lr;
+  __device__ __forceinline__ void operator()(const float (&x)[2],
+                                             float (&y)[1]) const {
+    const float t = x[1] * lr;
+    y[0] = x[0] - t;
+  }
+};
+
 } // namespace
 } // namespace nt
 
@@ -280,6 +291,23 @@ int nt_binary_bwd(int32_t op, const nt_view *g, const nt_view *a,
       }
       fail(NT_ERR_VALUE, "binary_bwd: unknown op");
     });
+  });
+}
+
+int nt_sgd_step(const nt_view *p, const nt_view *g, double lr) {
+  return guard([&] {
+    check_view(p, "sgd_step");
+    check_view(g, "sgd_step");
+    require_same_shape(p, g, "sgd_step");
+    require_same_dtype(p, g, "sgd_step");
+    if (p->dtype != NT_FLOAT32)
+      fail(NT_ERR_VALUE, "sgd_step: float32 parameters only");
+    const float lr32 = float(lr);
+    if (double(lr32) != lr)
+      fail(NT_ERR_VALUE, "sgd_step: lr must be a float32 value");
+    const nt_view *ins[2] = {p, g};
+    const nt_view *outs[1] = {p};
+    launch_elementwise<float, float, 2, 1>(ins, outs, SgdStep{lr32});
   });
 }
 

@@ -4,8 +4,13 @@ from __future__ import annotations
 
 from typing import Sequence
 
+import struct
+
+from .. import _kernels as K
 from .. import autograd as ag
+from .._data_type import Dtype
 from ..core import Tensor
+from ..cuda import Device
 
 
 class Optimizer:
@@ -32,9 +37,22 @@ class GradientDescent(Optimizer):
         self._lr = lr
 
     def step(self) -> None:
+        # lr as the reference's 0-d scalar tensor holds it (float32); a step
+        # size beyond float32's range takes the composition (an inf scalar)
+        try:
+            lr32 = struct.unpack("f", struct.pack("f", self._lr))[0]
+        except OverflowError:
+            lr32 = None
         for p in self.parameters:
             if p.requires_grad:
                 if p.grad is None:
                     raise RuntimeError("Gradients not set, did you call backward?")
+                g = p.grad
                 with ag.no_grad():
-                    p -= p.grad * self._lr
+                    if (lr32 is not None and p.device == Device.Cuda and g.device == Device.Cuda
+                            and p.dtype == Dtype.Float32 and g.dtype == Dtype.Float32
+                            and p.shape == g.shape):
+                        # one pass, same two roundings as the composition
+                        K.sgd_step(p, g, lr32)
+                    else:
+                        p -= g * self._lr

@@ -393,3 +393,29 @@ def test_config5_full_size_vs_cpu_reference(gpu):
         full_ulp = np.linalg.norm(np.spacing(np.abs(w0)).astype(np.float64))
         dn_ref = float(ref[f"dw{i}_norm64"])
         assert abs(dn - dn_ref) <= 1e-3 * dn_ref + np.sqrt(steps) * full_ulp, (i, dn, dn_ref)
+
+
+@pytest.mark.parametrize("shape,layout", [((1,), "contig"), ((7, 13), "contig"), ((1024, 4096), "contig"),
+                                          ((129, 300), "transposed"), ((4096,), "contig")])
+def test_sgd_step_fused_matches_composition(gpu, shape, layout):
+    # GradientDescent.step on float32 device parameters runs nt_sgd_step
+    # (one pass); it must equal the reference's p -= p.grad * lr bit for bit:
+    # the float32 product g * float32(lr), then the float32 difference
+    r = rng(seed_of("sgd", shape, layout))
+    lr = 1e-3
+    p0 = r.standard_normal(shape).astype(np.float32)
+    g0 = r.standard_normal(shape).astype(np.float32)
+    lr32 = np.float32(lr)
+    want = p0 - (g0 * lr32)  # numpy float32: one rounding per operation
+    p = dev(p0) if layout == "contig" else dev_T(p0)  # dev_T: a .T view
+    p.enable_grad()
+    p._grad = dev(g0)
+    v0 = p.version
+    nn.GradientDescent([p], lr=lr).step()
+    assert_bitexact(host(p), want, "sgd fused")
+    assert p.version == v0 + 1
+    # the composition on the device (the path float64 parameters take)
+    q = dev(p0)
+    with nt.no_grad():
+        q -= dev(g0) * lr
+    assert_bitexact(host(q), want, "sgd composition")
