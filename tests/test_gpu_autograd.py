@@ -419,3 +419,22 @@ def test_sgd_step_fused_matches_composition(gpu, shape, layout):
     with nt.no_grad():
         q -= dev(g0) * lr
     assert_bitexact(host(q), want, "sgd composition")
+
+
+def test_sgd_step_guards_and_float64_path(gpu):
+    from nanotorch_amd import _kernels as K
+    # nt_sgd_step takes float32 only, and lr as a float32 value
+    with pytest.raises(ValueError):
+        K.sgd_step(dev(np.zeros(4)), dev(np.zeros(4)), 0.5)
+    with pytest.raises(ValueError):
+        K.sgd_step(dev(np.zeros(4, np.float32)), dev(np.zeros(4, np.float32)), 0.1)
+    # float64 parameters take the reference's composition: g * float32(lr)
+    # promoted to float64, then the float64 difference
+    r = rng(seed_of("sgd64"))
+    p0, g0 = r.standard_normal(37), r.standard_normal(37)
+    p = dev(p0)
+    p.enable_grad()
+    p._grad = dev(g0)
+    nn.GradientDescent([p], lr=1e-3).step()
+    want = p0 - g0 * np.float64(np.float32(1e-3))
+    assert_bitexact(host(p), want, "sgd float64")
