@@ -231,3 +231,31 @@ def test_random_3d_permutes(gpu, case):
     wa, wb = O.bwd_binary(O.MUL, g, a, b)
     assert_bitexact(host(ta), O.accumulate(olds[0], wa), "mul bwd a " + tag)
     assert_bitexact(host(tb), O.accumulate(olds[1], wb), "mul bwd b " + tag)
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_random_3d_permute_reductions(gpu, case):
+    """sum / max / min / argmax / argmin of permuted 3-D views over axis
+    tuples in random order (the reduced index follows the tuple's order),
+    small integers so that ties occur and the first index must win."""
+    r = rng(6000 + case)
+    sides = [1, 2, 3, 8, 17, 64, 65, 130]
+    base_shape = tuple(int(r.choice(sides)) for _ in range(3))
+    perm = PERMS[int(r.integers(len(PERMS)))]
+    # |values| <= 3: every partial sum of at most 130^3 of them is an
+    # integer below 2^24, exact in fp32 whatever the summation order
+    a0 = r.integers(-3, 4, base_shape).astype(np.float32)
+    x = _permute(dev(a0), perm)
+    a = np.ascontiguousarray(a0.transpose(perm))
+    naxes = int(r.integers(1, 4))
+    axes = tuple(int(v) for v in r.permutation(3)[:naxes])
+    kshape = tuple(s for i, s in enumerate(a.shape) if i not in axes)
+    tag = f"case {case} base {base_shape} perm {perm} axes={axes}"
+    got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, axes, nt.float32), kshape))
+    assert_bitexact(got, O.reduce(O.R_SUM, a, axes, np.float32), "sum " + tag)
+    for op, oop, aop in ((_lib.R_MAX, O.R_MAX, O.R_ARGMAX), (_lib.R_MIN, O.R_MIN, O.R_ARGMIN)):
+        v, idx, cnt = K.reduce(op, x, axes, nt.float32, want_aux=True)
+        assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), O.reduce(oop, a, axes),
+                        f"{op} value " + tag)
+        assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(aop, a, axes),
+                        f"{op} index " + tag)
