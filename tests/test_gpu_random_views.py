@@ -235,9 +235,10 @@ def test_random_3d_permutes(gpu, case):
 
 @pytest.mark.parametrize("case", range(30))
 def test_random_3d_permute_reductions(gpu, case):
-    """sum / max / min / argmax / argmin of permuted 3-D views over axis
-    tuples in random order (the reduced index follows the tuple's order),
-    small integers so that ties occur and the first index must win."""
+    """sum / max / min / argmax / argmin, the counts and the max/min
+    backward of permuted 3-D views over axis tuples in random order (the
+    reduced index follows the tuple's order), small integers so that ties
+    occur: the first index must win and a tied slice routes no gradient."""
     r = rng(6000 + case)
     sides = [1, 2, 3, 8, 17, 64, 65, 130]
     base_shape = tuple(int(r.choice(sides)) for _ in range(3))
@@ -253,9 +254,26 @@ def test_random_3d_permute_reductions(gpu, case):
     tag = f"case {case} base {base_shape} perm {perm} axes={axes}"
     got = host(nt.Tensor._new_contiguous(K.reduce(_lib.R_SUM, x, axes, nt.float32), kshape))
     assert_bitexact(got, O.reduce(O.R_SUM, a, axes, np.float32), "sum " + tag)
+    shape = a.shape
+    gshape = tuple(1 if i in axes else d for i, d in enumerate(shape))
+    g = r.standard_normal(kshape).astype(np.float32)
     for op, oop, aop in ((_lib.R_MAX, O.R_MAX, O.R_ARGMAX), (_lib.R_MIN, O.R_MIN, O.R_ARGMIN)):
         v, idx, cnt = K.reduce(op, x, axes, nt.float32, want_aux=True)
         assert_bitexact(host(nt.Tensor._new_contiguous(v, kshape)), O.reduce(oop, a, axes),
                         f"{op} value " + tag)
         assert_bitexact(host(nt.Tensor._new_contiguous(idx, kshape)), O.reduce(aop, a, axes),
                         f"{op} index " + tag)
+        ext = O.reduce(oop, a, axes).reshape(gshape)
+        want_cnt = (a == ext).sum(axis=axes).astype(np.int32).reshape(kshape)
+        assert_bitexact(host(nt.Tensor._new_contiguous(cnt, kshape)), want_cnt, f"{op} count " + tag)
+        # backward: g routed to the single extremum of each slice, 0 for a
+        # slice with ties; into a new buffer, then accumulated into a target
+        # laid out like x (permuted)
+        want = O.sel_bwd(oop, g, a, axes)
+        st = K.reduce_bwd(op, dev(g), 1.0, idx, cnt, axes, shape, None)
+        assert_bitexact(host(nt.Tensor._new_contiguous(st, shape)), want, f"{op} bwd " + tag)
+        old0 = r.standard_normal(base_shape).astype(np.float32)
+        tgt = _permute(dev(old0), perm)
+        K.reduce_bwd(op, dev(g), 1.0, idx, cnt, axes, shape, tgt)
+        old = np.ascontiguousarray(old0.transpose(perm))
+        assert_bitexact(host(tgt), O.accumulate(old, want), f"{op} bwd acc " + tag)
