@@ -438,3 +438,63 @@ def test_sgd_step_guards_and_float64_path(gpu):
     nn.GradientDescent([p], lr=1e-3).step()
     want = p0 - g0 * np.float64(np.float32(1e-3))
     assert_bitexact(host(p), want, "sgd float64")
+
+
+_CHAIN_UNARY = {  # name: (Tensor op, oracle op, oracle backward of (g, input, output))
+    "neg": (lambda t: -t, O.NEG, lambda g, x, y: O.bwd_neg(g)),
+    "tanh": (nt.tanh, O.TANH, lambda g, x, y: O.bwd_tanh(g, y)),
+    "sigmoid": (nt.sigmoid, O.SIGMOID, lambda g, x, y: O.bwd_sigmoid(g, y)),
+    "relu": (nt.relu, O.RELU, lambda g, x, y: O.bwd_relu(g, y)),
+}
+_CHAIN_BINARY = {"add": (lambda a, b: a + b, O.ADD), "sub": (lambda a, b: a - b, O.SUB),
+                 "mul": (lambda a, b: a * b, O.MUL)}
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_chains_vs_oracle(gpu, case):
+    """Seeded random chains of 3-6 ops on [R, C] tensors (contiguous or .T
+    leaves), loss = sum: the engine, the fused backward kernels and their
+    layouts against the oracle's per-op chains composed in reverse.  Every
+    leaf is used once (no accumulation order to match); forwards of tanh /
+    sigmoid come from different math libraries, hence the tolerance."""
+    r = rng(7000 + case)
+    R, C = (int(v) for v in r.choice([3, 17, 64, 129, 256], 2))
+    def leaf():
+        a = r.standard_normal((R, C)).astype(np.float32)
+        t = dev(a) if r.random() < 0.5 else dev_T(a)
+        t.enable_grad()
+        return t, a
+    x, xa = leaf()
+    nodes = []  # (kind, name, oracle input(s), oracle output, index of y's leaf)
+    t, ta = x, xa
+    leaves = [(x, xa)]
+    for _ in range(int(r.integers(3, 7))):
+        if r.random() < 0.5:
+            name = str(r.choice(list(_CHAIN_UNARY)))
+            fn, oop, _ = _CHAIN_UNARY[name]
+            t2, a2 = fn(t), O.unary(oop, ta)
+            nodes.append(("u", name, ta, a2, None))
+        else:
+            name = str(r.choice(list(_CHAIN_BINARY)))
+            fn, oop = _CHAIN_BINARY[name]
+            y, ya = leaf()
+            leaves.append((y, ya))
+            t2, a2 = fn(t, y), O.binary(oop, ta, ya)
+            nodes.append(("b", name, (ta, ya), a2, len(leaves) - 1))
+        t, ta = t2, a2
+    t.sum().backward()
+    # oracle: d(sum)/dt = 1, then each node's backward in reverse
+    g = np.ones((R, C), np.float32)
+    want = [None] * len(leaves)
+    for kind, name, ins, out, yi in reversed(nodes):
+        if kind == "u":
+            g = _CHAIN_UNARY[name][2](g, ins, out)
+        else:
+            ga, gb = O.bwd_binary(_CHAIN_BINARY[name][1], g, ins[0], ins[1])
+            want[yi] = gb
+            g = ga
+    want[0] = g
+    tag = f"case {case} [{R},{C}] ops {[n[1] for n in nodes]}"
+    for i, (leaf_t, _) in enumerate(leaves):
+        got = host(leaf_t.grad)
+        assert_rel(got, want[i], 1e-4, f"grad {i} " + tag, scale=np.abs(want[i]) + 1e-3)
