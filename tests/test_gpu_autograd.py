@@ -498,3 +498,66 @@ def test_random_chains_vs_oracle(gpu, case):
     for i, (leaf_t, _) in enumerate(leaves):
         got = host(leaf_t.grad)
         assert_rel(got, want[i], 1e-4, f"grad {i} " + tag, scale=np.abs(want[i]) + 1e-3)
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_random_chains_reduced_vs_oracle(gpu, case):
+    """Random chains as above, ending in a reduction along one axis before
+    the sum: mean (any op) or max (correctly rounded ops only, so that the
+    device and the oracle see the same values and route the gradient to the
+    same element, a tied slice getting none)."""
+    r = rng(7500 + case)
+    use_max = case % 2 == 1
+    R, C = (int(v) for v in r.choice([3, 17, 64, 129], 2))
+    def leaf():
+        # max: small integers, so that ties occur
+        a = (r.integers(-4, 5, (R, C)) if use_max else r.standard_normal((R, C))).astype(np.float32)
+        t = dev(a) if r.random() < 0.5 else dev_T(a)
+        t.enable_grad()
+        return t, a
+    unary = ["neg", "relu"] if use_max else list(_CHAIN_UNARY)
+    x, xa = leaf()
+    leaves, nodes = [(x, xa)], []
+    t, ta = x, xa
+    for _ in range(int(r.integers(2, 5))):
+        if r.random() < 0.5:
+            name = str(r.choice(unary))
+            fn, oop, _ = _CHAIN_UNARY[name]
+            t2, a2 = fn(t), O.unary(oop, ta)
+            nodes.append(("u", name, ta, a2, None))
+        else:
+            name = str(r.choice(list(_CHAIN_BINARY)))
+            fn, oop = _CHAIN_BINARY[name]
+            y, ya = leaf()
+            leaves.append((y, ya))
+            t2, a2 = fn(t, y), O.binary(oop, ta, ya)
+            nodes.append(("b", name, (ta, ya), a2, len(leaves) - 1))
+        t, ta = t2, a2
+    ax = int(r.integers(0, 2))
+    kshape = (C,) if ax == 0 else (R,)
+    ones = np.ones(kshape, np.float32)
+    if use_max:
+        t.max(axis=ax).sum().backward()
+        g = O.sel_bwd(O.R_MAX, ones, ta, (ax,))
+    else:
+        t.mean(axis=ax).sum().backward()
+        n = ta.shape[ax]
+        gshape = (1, C) if ax == 0 else (R, 1)
+        gb = np.broadcast_to(ones.reshape(gshape), ta.shape)
+        g = O.binary(O.DIV, gb, np.broadcast_to(O.scalar(n, np.float32), ta.shape))
+    want = [None] * len(leaves)
+    for kind, name, ins, out, yi in reversed(nodes):
+        if kind == "u":
+            g = _CHAIN_UNARY[name][2](g, ins, out)
+        else:
+            ga, gb_ = O.bwd_binary(_CHAIN_BINARY[name][1], g, ins[0], ins[1])
+            want[yi] = gb_
+            g = ga
+    want[0] = g
+    tag = f"case {case} [{R},{C}] {'max' if use_max else 'mean'} axis {ax} ops {[n[1] for n in nodes]}"
+    for i, (leaf_t, _) in enumerate(leaves):
+        got = host(leaf_t.grad)
+        if use_max:
+            assert_bitexact(got, want[i], f"grad {i} " + tag)
+        else:
+            assert_rel(got, want[i], 1e-4, f"grad {i} " + tag, scale=np.abs(want[i]) + 1e-6)
