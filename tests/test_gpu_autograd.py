@@ -561,3 +561,55 @@ def test_random_chains_reduced_vs_oracle(gpu, case):
             assert_bitexact(got, want[i], f"grad {i} " + tag)
         else:
             assert_rel(got, want[i], 1e-4, f"grad {i} " + tag, scale=np.abs(want[i]) + 1e-6)
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_random_chains_with_transposes_vs_oracle(gpu, case):
+    """Random chains with `.T` steps in between: the gradient reaching the
+    fused backward kernels is then itself a transposed view, and leaves of
+    later binary ops take the transposed shape."""
+    r = rng(7800 + case)
+    shape = tuple(int(v) for v in r.choice([3, 17, 64, 129], 2))
+    def leaf(sh):
+        a = r.standard_normal(sh).astype(np.float32)
+        t = dev(a) if r.random() < 0.5 else dev_T(a)
+        t.enable_grad()
+        return t, a
+    x, xa = leaf(shape)
+    leaves, nodes = [(x, xa)], []
+    t, ta = x, xa
+    for _ in range(int(r.integers(3, 7))):
+        u = r.random()
+        if u < 0.3:
+            t2, a2 = t.T, np.ascontiguousarray(ta.T)
+            nodes.append(("T", "T", None, None, None))
+        elif u < 0.65:
+            name = str(r.choice(list(_CHAIN_UNARY)))
+            fn, oop, _ = _CHAIN_UNARY[name]
+            t2, a2 = fn(t), O.unary(oop, ta)
+            nodes.append(("u", name, ta, a2, None))
+        else:
+            name = str(r.choice(list(_CHAIN_BINARY)))
+            fn, oop = _CHAIN_BINARY[name]
+            y, ya = leaf(ta.shape)
+            leaves.append((y, ya))
+            t2, a2 = fn(t, y), O.binary(oop, ta, ya)
+            nodes.append(("b", name, (ta, ya), a2, len(leaves) - 1))
+        t, ta = t2, a2
+    t.sum().backward()
+    g = np.ones(ta.shape, np.float32)
+    want = [None] * len(leaves)
+    for kind, name, ins, out, yi in reversed(nodes):
+        if kind == "T":
+            g = np.ascontiguousarray(g.T)
+        elif kind == "u":
+            g = _CHAIN_UNARY[name][2](g, ins, out)
+        else:
+            ga, gb = O.bwd_binary(_CHAIN_BINARY[name][1], g, ins[0], ins[1])
+            want[yi] = gb
+            g = ga
+    want[0] = g
+    tag = f"case {case} {shape} ops {[n[1] for n in nodes]}"
+    for i, (leaf_t, _) in enumerate(leaves):
+        got = host(leaf_t.grad)
+        assert_rel(got, want[i], 1e-4, f"grad {i} " + tag, scale=np.abs(want[i]) + 1e-3)
