@@ -613,3 +613,57 @@ def test_random_chains_with_transposes_vs_oracle(gpu, case):
     for i, (leaf_t, _) in enumerate(leaves):
         got = host(leaf_t.grad)
         assert_rel(got, want[i], 1e-4, f"grad {i} " + tag, scale=np.abs(want[i]) + 1e-3)
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_random_chains_with_broadcast_vs_oracle(gpu, case):
+    """Random chains whose binary ops take a broadcast row [1, C] or column
+    [R, 1] as their second operand: that operand's gradient is the
+    unbroadcast sum over the broadcast axis (its order differs from the
+    reference's sequential sum, hence a bound scaled by the sum of |terms|)."""
+    r = rng(8100 + case)
+    R, C = (int(v) for v in r.choice([3, 17, 64, 129], 2))
+    x0 = r.standard_normal((R, C)).astype(np.float32)
+    x = dev(x0) if r.random() < 0.5 else dev_T(x0)
+    x.enable_grad()
+    leaves, nodes = [(x, x0, None)], []
+    t, ta = x, x0
+    for _ in range(int(r.integers(3, 7))):
+        if r.random() < 0.45:
+            name = str(r.choice(list(_CHAIN_UNARY)))
+            fn, oop, _ = _CHAIN_UNARY[name]
+            t2, a2 = fn(t), O.unary(oop, ta)
+            nodes.append(("u", name, ta, a2, None))
+        else:
+            name = str(r.choice(list(_CHAIN_BINARY)))
+            fn, oop = _CHAIN_BINARY[name]
+            bshape = [(1, C), (R, 1), (R, C)][int(r.integers(3))]
+            ya = r.standard_normal(bshape).astype(np.float32)
+            y = dev(ya)
+            y.enable_grad()
+            axes = tuple(i for i in (0, 1) if bshape[i] == 1 and (R, C)[i] != 1)
+            leaves.append((y, ya, axes))
+            yb = np.ascontiguousarray(np.broadcast_to(ya, (R, C)))
+            t2, a2 = fn(t, y), O.binary(oop, ta, yb)
+            nodes.append(("b", name, (ta, yb), a2, len(leaves) - 1))
+        t, ta = t2, a2
+    t.sum().backward()
+    g = np.ones((R, C), np.float32)
+    want, scale = [None] * len(leaves), [None] * len(leaves)
+    for kind, name, ins, out, yi in reversed(nodes):
+        if kind == "u":
+            g = _CHAIN_UNARY[name][2](g, ins, out)
+            continue
+        ga, gb = O.bwd_binary(_CHAIN_BINARY[name][1], g, ins[0], ins[1])
+        axes, shp = leaves[yi][2], leaves[yi][1].shape
+        if axes:
+            want[yi] = O.reduce(O.R_SUM, gb, axes, np.float32).reshape(shp)
+            scale[yi] = O.reduce(O.R_SUM, np.abs(gb).astype(np.float64), axes, np.float64).reshape(shp)
+        else:
+            want[yi], scale[yi] = gb.reshape(shp), np.abs(gb).reshape(shp)
+        g = ga
+    want[0], scale[0] = g, np.abs(g)
+    tag = f"case {case} [{R},{C}] ops {[n[1] for n in nodes]}"
+    for i, (leaf_t, _, _) in enumerate(leaves):
+        got = host(leaf_t.grad)
+        assert_rel(got, want[i], 1e-4, f"grad {i} " + tag, scale=scale[i] + 1e-3)
