@@ -667,3 +667,49 @@ def test_random_chains_with_broadcast_vs_oracle(gpu, case):
     for i, (leaf_t, _, _) in enumerate(leaves):
         got = host(leaf_t.grad)
         assert_rel(got, want[i], 1e-4, f"grad {i} " + tag, scale=scale[i] + 1e-3)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_chains_with_matmul_vs_oracle(gpu, case):
+    """Random chains with one matmul step t @ W (W a leaf, contiguous or a
+    .T view) between elementwise ops: dA = G . W^T and dW = t^T . G through
+    the engine against the oracle's sequential products (the device sums
+    in another order: bounds scaled by the products of |values|)."""
+    r = rng(8400 + case)
+    R, C, D = (int(v) for v in r.choice([3, 17, 64, 129, 256], 3))
+    def mk(a):
+        t = dev(a) if r.random() < 0.5 else dev_T(a)
+        t.enable_grad()
+        return t
+    x0 = r.standard_normal((R, C)).astype(np.float32)
+    w0 = (r.standard_normal((C, D)) / np.sqrt(C)).astype(np.float32)
+    x, w = mk(x0), mk(w0)
+    pre = [str(r.choice(list(_CHAIN_UNARY))) for _ in range(int(r.integers(0, 3)))]
+    post = [str(r.choice(list(_CHAIN_UNARY))) for _ in range(int(r.integers(1, 3)))]
+    t, ta, acts = x, x0, []
+    for name in pre:
+        t2, a2 = _CHAIN_UNARY[name][0](t), O.unary(_CHAIN_UNARY[name][1], ta)
+        acts.append((name, ta, a2))
+        t, ta = t2, a2
+    m_in = ta
+    t, ta = t @ w, O.matmul(ta, w0, parallel=True)
+    m_out_acts = []
+    for name in post:
+        t2, a2 = _CHAIN_UNARY[name][0](t), O.unary(_CHAIN_UNARY[name][1], ta)
+        m_out_acts.append((name, ta, a2))
+        t, ta = t2, a2
+    t.sum().backward()
+    g = np.ones(ta.shape, np.float32)
+    for name, ins, out in reversed(m_out_acts):
+        g = _CHAIN_UNARY[name][2](g, ins, out)
+    gw = O.matmul(np.ascontiguousarray(m_in.T), g, parallel=True)
+    gw_scale = O.matmul(np.abs(m_in.T).astype(np.float32), np.abs(g), parallel=True)
+    gx = O.matmul(g, np.ascontiguousarray(w0.T), parallel=True)
+    gx_scale = O.matmul(np.abs(g), np.abs(w0.T).astype(np.float32), parallel=True)
+    for name, ins, out in reversed(acts):
+        # tanh, sigmoid, relu and neg have |derivative| <= 1, so the
+        # product's error bound carries through their backwards unscaled
+        gx = _CHAIN_UNARY[name][2](gx, ins, out)
+    tag = f"case {case} ({R},{C},{D}) pre {pre} post {post}"
+    assert_rel(host(w.grad), gw, 1e-4, "dW " + tag, scale=gw_scale + 1e-4)
+    assert_rel(host(x.grad), gx, 1e-4, "dx " + tag, scale=gx_scale + np.abs(gx) + 1e-4)
