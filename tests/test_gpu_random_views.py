@@ -277,3 +277,39 @@ def test_random_3d_permute_reductions(gpu, case):
         K.reduce_bwd(op, dev(g), 1.0, idx, cnt, axes, shape, tgt)
         old = np.ascontiguousarray(old0.transpose(perm))
         assert_bitexact(host(tgt), O.accumulate(old, want), f"{op} bwd acc " + tag)
+
+
+_DTS = [np.int32, np.int64, np.float32, np.float64]  # the reference's order
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_mixed_dtype_binary(gpu, case):
+    """Binary ops and comparisons between tensors of different dtypes, in
+    either layout: the Python layer promotes to max(dtype) (int32 < int64 <
+    float32 < float64) and casts with the reference's static_cast (large
+    int64 values round to float32), then the device kernel runs; against
+    numpy's casts and the oracle in the promoted dtype."""
+    r = rng(8800 + case)
+    shape = (int(r.choice([1, 7, 64, 257])), int(r.choice([1, 5, 64, 130])))
+    i, j = int(r.integers(4)), int(r.integers(4))
+    name = str(r.choice(["add", "sub", "mul", "gt", "ge", "eq"]))
+    big = 2**40 if name != "mul" else 2**15  # int64 sums past float32's 24 bits
+    def draw(dt):
+        if dt == np.int32:
+            return r.integers(-2**15, 2**15, shape).astype(np.int32)
+        if dt == np.int64:
+            return r.integers(-big, big, shape).astype(np.int64)
+        return (r.standard_normal(shape) * 100).astype(dt)
+    a, b = draw(_DTS[i]), draw(_DTS[j])
+    if name in ("gt", "ge", "eq"):
+        b[::2] = a[::2].astype(b.dtype)  # some equal pairs (after the cast)
+    xa = dev(a) if r.random() < 0.5 else dev_T(a)
+    xb = dev(b) if r.random() < 0.5 else dev_T(b)
+    pd = _DTS[max(i, j)]
+    ops = {"add": (lambda p, q: p + q, O.ADD), "sub": (lambda p, q: p - q, O.SUB),
+           "mul": (lambda p, q: p * q, O.MUL), "gt": (lambda p, q: p > q, O.GT),
+           "ge": (lambda p, q: p >= q, O.GE), "eq": (lambda p, q: p == q, O.EQ)}
+    fn, oop = ops[name]
+    got = host(fn(xa, xb))
+    want = O.binary(oop, a.astype(pd), b.astype(pd))
+    assert_bitexact(got, want, f"case {case} {name} {a.dtype}/{b.dtype} {shape}")
