@@ -313,3 +313,39 @@ def test_random_mixed_dtype_binary(gpu, case):
     got = host(fn(xa, xb))
     want = O.binary(oop, a.astype(pd), b.astype(pd))
     assert_bitexact(got, want, f"case {case} {name} {a.dtype}/{b.dtype} {shape}")
+
+
+_CAST_DTS = [(np.bool_, nt.bool_), (np.int32, nt.int32), (np.int64, nt.int64),
+             (np.float32, nt.float32), (np.float64, nt.float64)]
+
+
+@pytest.mark.parametrize("case", range(20))
+def test_random_device_casts(gpu, case):
+    """Tensor.to(dtype) on the device from contiguous, .T and sliced views,
+    every pair of dtypes: the reference's Storage::cast (static_cast; to bool
+    s != 0, so NaN and -0.0 map as C++ does), values kept inside the target
+    range; against numpy's C casts."""
+    r = rng(9100 + case)
+    shape = (int(r.choice([1, 6, 64, 130])), int(r.choice([1, 3, 64, 257])))
+    (snp, _), (dnp, dnt) = (_CAST_DTS[int(r.integers(5))], _CAST_DTS[int(r.integers(5))])
+    if snp == np.bool_:
+        a = r.random(shape) < 0.5
+    elif np.issubdtype(snp, np.integer):
+        a = r.integers(-3000, 3000, shape).astype(snp)
+        a[0, 0] = 0
+    else:
+        a = (r.standard_normal(shape) * 1000).astype(snp)
+        a.flat[0] = -0.0
+        if dnp == np.bool_:
+            a.flat[-1] = np.nan  # static_cast<bool>(NaN) is true
+    kind = str(r.choice(["contig", "T", "slice"]))
+    if kind == "T":
+        x = dev_T(a)
+    elif kind == "slice":
+        big = np.repeat(a, 2, axis=1)
+        x, a = dev(big)[:, ::2], big[:, ::2]
+    else:
+        x = dev(a)
+    got = host(x.to(dnt))
+    want = (a != 0) if dnp == np.bool_ else a.astype(dnp)
+    assert_bitexact(got, np.asarray(want, dtype=dnp), f"case {case} {a.dtype}->{np.dtype(dnp)} {kind} {shape}")
