@@ -349,3 +349,55 @@ def test_random_device_casts(gpu, case):
     got = host(x.to(dnt))
     want = (a != 0) if dnp == np.bool_ else a.astype(dnp)
     assert_bitexact(got, np.asarray(want, dtype=dnp), f"case {case} {a.dtype}->{np.dtype(dnp)} {kind} {shape}")
+
+
+def _writable(r, shape, kind):
+    """(device view, numpy copy of it, device base, numpy copy of the base,
+    the base elements the view does not cover) of a writable target laid
+    out as `kind`."""
+    R, C = shape
+    if kind == "T":
+        a = _values(r, shape)
+        d = dev_T(a)
+        return d, a.copy(), d, a.copy(), lambda full: full[:0]
+    if kind == "slice":
+        big = _values(r, (R, 2 * C))
+        d = dev(big)
+        return d[:, ::2], np.ascontiguousarray(big[:, ::2]), d, big.copy(), lambda full: full[:, 1::2]
+    if kind == "offset":
+        flat = _values(r, (R * C + 1,))
+        d = dev(flat)
+        return d[1:].reshape(R, C), flat[1:].reshape(R, C).copy(), d, flat.copy(), lambda full: full[:1]
+    a = _values(r, shape)
+    d = dev(a)
+    return d, a.copy(), d, a.copy(), lambda full: full[:0]
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_inplace_on_views(gpu, case):
+    """out op= other with out a contiguous, .T, sliced or misaligned view and
+    other in any of the seven layouts (broadcasts included): the in-place
+    kernels write through strided targets (tile and flat kernels, one output
+    that is also an input); the elements outside the view stay untouched."""
+    r = rng(9400 + case)
+    shape = (int(r.choice(SIDES)), int(r.choice(SIDES)))
+    tk = str(r.choice(["contig", "T", "slice", "offset"]))
+    ok = str(r.choice(KINDS))
+    name = str(r.choice(["add", "sub", "mul", "div"]))
+    out, want, base, base_np, untouched = _writable(r, shape, tk)
+    other, b = _operand(r, shape, ok, positive=(name == "div"))
+    oop = {"add": O.ADD, "sub": O.SUB, "mul": O.MUL, "div": O.DIV}[name]
+    with nt.no_grad():
+        if name == "add":
+            out += other
+        elif name == "sub":
+            out -= other
+        elif name == "mul":
+            out *= other
+        else:
+            out /= other
+    O.inplace(oop, want, b)
+    tag = f"case {case} {name} out {tk} other {ok} {shape}"
+    assert_bitexact(host(out), want, tag)
+    assert_bitexact(np.ascontiguousarray(untouched(host(base))),
+                    np.ascontiguousarray(untouched(base_np)), "outside the view " + tag)
