@@ -713,3 +713,53 @@ def test_random_chains_with_matmul_vs_oracle(gpu, case):
     tag = f"case {case} ({R},{C},{D}) pre {pre} post {post}"
     assert_rel(host(w.grad), gw, 1e-4, "dW " + tag, scale=gw_scale + 1e-4)
     assert_rel(host(x.grad), gx, 1e-4, "dx " + tag, scale=gx_scale + np.abs(gx) + 1e-4)
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_random_api_reductions_vs_oracle(gpu, case):
+    """sum / mean / max / min through the Tensor methods with axis given as
+    an int, a negative int, a tuple or None and keepdim either way, then
+    backward of (out * G).sum() for a random G: the Python layer's axis
+    handling and reshapes around the reduction kernels and their backwards."""
+    r = rng(9700 + case)
+    shape = tuple(int(v) for v in r.choice([2, 3, 17, 64], 3))
+    a = r.integers(-4, 5, shape).astype(np.float32)  # small integers: exact sums, ties
+    x = dev(a)
+    x.enable_grad()
+    form = int(r.integers(4))
+    if form == 0:
+        axis = int(r.integers(3))
+        axes = (axis,)
+    elif form == 1:
+        axis = -int(r.integers(1, 4))
+        axes = (axis % 3,)
+    elif form == 2:
+        axes = tuple(int(v) for v in r.permutation(3)[:2])
+        axis = axes
+    else:
+        axis, axes = None, (0, 1, 2)
+    keepdim = bool(r.integers(2))
+    name = str(r.choice(["sum", "mean", "max", "min"]))
+    if name in ("max", "min") and isinstance(axis, tuple):
+        axis, axes = axes[0], (axes[0],)  # max/min take one axis or None
+    out = getattr(x, name)(axis=axis, keepdim=keepdim)
+    kshape = tuple(1 if i in axes else d for i, d in enumerate(shape)) if keepdim \
+        else tuple(d for i, d in enumerate(shape) if i not in axes)
+    assert out.shape == kshape, (out.shape, kshape)
+    oop = {"sum": O.R_SUM, "mean": O.R_SUM, "max": O.R_MAX, "min": O.R_MIN}[name]
+    red = O.reduce(oop, a, tuple(sorted(axes)), np.float32 if oop == O.R_SUM else None)
+    n = int(np.prod([shape[i] for i in axes]))
+    fwd = red if name != "mean" else O.binary(O.DIV, red, np.broadcast_to(O.scalar(n, np.float32), red.shape))
+    tag = f"case {case} {name} axis={axis} keepdim={keepdim} {shape}"
+    assert_bitexact(host(out).reshape(-1), np.ascontiguousarray(fwd).reshape(-1), "fwd " + tag)
+    G0 = r.standard_normal(kshape).astype(np.float32)
+    (out * dev(G0)).sum().backward()
+    gk = G0.reshape(tuple(1 if i in axes else d for i, d in enumerate(shape)))
+    gb = np.ascontiguousarray(np.broadcast_to(gk, shape))
+    if name == "sum":
+        want = gb
+    elif name == "mean":
+        want = O.binary(O.DIV, gb, np.broadcast_to(O.scalar(n, np.float32), shape))
+    else:
+        want = O.sel_bwd(oop, G0.reshape(tuple(d for i, d in enumerate(shape) if i not in axes)), a, axes)
+    assert_bitexact(host(x.grad), np.ascontiguousarray(want).reshape(shape), "bwd " + tag)
