@@ -763,3 +763,54 @@ def test_random_api_reductions_vs_oracle(gpu, case):
     else:
         want = O.sel_bwd(oop, G0.reshape(tuple(d for i, d in enumerate(shape) if i not in axes)), a, axes)
     assert_bitexact(host(x.grad), np.ascontiguousarray(want).reshape(shape), "bwd " + tag)
+
+
+def _sum_to(g: np.ndarray, shape) -> np.ndarray:
+    """g summed over the axes broadcasting added to reach it from `shape`."""
+    while g.ndim > len(shape):
+        g = g.sum(axis=0)
+    for i, d in enumerate(shape):
+        if d == 1 and g.shape[i] != 1:
+            g = g.sum(axis=i, keepdims=True)
+    return g
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_api_matmul_vs_oracle(gpu, case):
+    """a @ b through the Tensor operator with 1-D operands and broadcast
+    batch dims (the reference's _matmul_broadcast rules), forward and both
+    gradients of (out * G).sum() (unbroadcast over the batch dims), against
+    float64 products with bounds scaled by the products of |values|."""
+    r = rng(9900 + case)
+    n, k, m = (int(v) for v in r.choice([1, 3, 16, 33], 3))
+    batches = [(), (2,), (3, 1), (1, 4), (3, 4)]
+    ba, bb = batches[int(r.integers(5))], batches[int(r.integers(5))]
+    try:
+        np.broadcast_shapes(ba, bb)
+    except ValueError:
+        bb = ()
+    a_shape = (k,) if r.random() < 0.2 else (*ba, n, k)
+    b_shape = (k,) if r.random() < 0.2 else (*bb, k, m)
+    a0 = r.standard_normal(a_shape).astype(np.float32)
+    b0 = r.standard_normal(b_shape).astype(np.float32)
+    xa, xb = dev(a0), dev(b0)
+    xa.enable_grad()
+    xb.enable_grad()
+    out = xa @ xb
+    want = np.matmul(a0.astype(np.float64), b0.astype(np.float64))
+    scale = np.matmul(np.abs(a0).astype(np.float64), np.abs(b0).astype(np.float64))
+    tag = f"case {case} {a_shape} @ {b_shape}"
+    assert out.shape == want.shape, (out.shape, want.shape, tag)
+    assert_rel(host(out), want, 1e-5, "fwd " + tag, scale=scale + 1e-6)
+    G = r.standard_normal(want.shape).astype(np.float32)
+    (out * dev(G)).sum().backward()
+    # 1-D operands as the (1, k) row / (k, 1) column they are promoted to
+    A2 = a0[None, :] if a0.ndim == 1 else a0
+    B2 = b0[:, None] if b0.ndim == 1 else b0
+    G2 = G.reshape(np.matmul(A2, B2).shape).astype(np.float64)
+    gA = _sum_to(np.matmul(G2, np.swapaxes(B2, -1, -2).astype(np.float64)), A2.shape).reshape(a_shape)
+    sA = _sum_to(np.matmul(np.abs(G2), np.abs(np.swapaxes(B2, -1, -2)).astype(np.float64)), A2.shape).reshape(a_shape)
+    gB = _sum_to(np.matmul(np.swapaxes(A2, -1, -2).astype(np.float64), G2), B2.shape).reshape(b_shape)
+    sB = _sum_to(np.matmul(np.abs(np.swapaxes(A2, -1, -2)).astype(np.float64), np.abs(G2)), B2.shape).reshape(b_shape)
+    assert_rel(host(xa.grad), gA, 1e-5, "dA " + tag, scale=sA + 1e-6)
+    assert_rel(host(xb.grad), gB, 1e-5, "dB " + tag, scale=sB + 1e-6)
