@@ -814,3 +814,29 @@ def test_random_api_matmul_vs_oracle(gpu, case):
     sB = _sum_to(np.matmul(np.abs(np.swapaxes(A2, -1, -2)).astype(np.float64), np.abs(G2)), B2.shape).reshape(b_shape)
     assert_rel(host(xa.grad), gA, 1e-5, "dA " + tag, scale=sA + 1e-6)
     assert_rel(host(xb.grad), gB, 1e-5, "dB " + tag, scale=sB + 1e-6)
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_random_mlps_vs_oracle(gpu, case):
+    """Random small MLPs (2-4 Linear layers of odd widths, so every matmul
+    kernel meets partial tiles; random activations) trained for 5 SGD steps
+    with the one-pass update: per-step losses and final weights against the
+    oracle's training step, as for config 1."""
+    r = rng(9950 + case)
+    nl = int(r.integers(2, 5))
+    dims = [int(v) for v in r.choice([5, 17, 33, 64, 100, 129, 260], nl + 1)]
+    acts = [str(v) for v in r.choice(["relu", "tanh", "sigmoid"], nl - 1)]
+    batch = int(r.choice([8, 31, 64, 130]))
+    x = r.standard_normal((batch, dims[0])).astype(np.float32)
+    t = r.standard_normal((batch, dims[-1])).astype(np.float32)
+    params = _mlp_params(r, dims)
+    lr = 0.05
+    got_losses, got_params = _run_mlp([(W.copy(), b.copy()) for W, b in params], x, t, acts, lr, 5)
+    ref = [(W.copy(), b.copy()) for W, b in params]
+    ref_losses = [float(O.mlp_step(ref, x, t, acts, lr)) for _ in range(5)]
+    tag = f"case {case} dims {dims} acts {acts} batch {batch}"
+    for i, (g, w) in enumerate(zip(got_losses, ref_losses)):
+        assert abs(g - w) <= 1e-4 * abs(w), (tag, i, g, w)
+    for (gW, gb), (rW, rb) in zip(got_params, ref):
+        assert np.allclose(gW, rW, rtol=1e-3, atol=1e-5), tag
+        assert np.allclose(gb, rb, rtol=1e-3, atol=1e-5), tag
