@@ -166,3 +166,47 @@ def test_row_gather_scatter_vector_path(gpu, dtype):
         want = table.copy()
         want[uniq] = vals
         assert_bitexact(t.numpy(), want, f"scatter {width} {off}")
+
+
+def _random_selector(r, shape):
+    """A random index tuple: per axis an int, a slice (any step sign), an
+    index list (negative entries and repeats allowed; all lists of one
+    selector share a length so that they broadcast) or the whole axis."""
+    nfancy_len = int(r.integers(1, 7))
+    sel = []
+    for d in shape[: int(r.integers(1, len(shape) + 1))]:
+        u = r.random()
+        if u < 0.2:
+            sel.append(int(r.integers(-d, d)))
+        elif u < 0.45:
+            start, stop = (int(v) for v in r.integers(-d, d + 1, 2))
+            step = int(r.choice([1, 2, 3, -1, -2]))
+            sel.append(slice(start, stop, step))
+        elif u < 0.8:
+            sel.append([int(v) for v in r.integers(-d, d, nfancy_len)])
+        else:
+            sel.append(slice(None))
+    return tuple(sel)
+
+
+@pytest.mark.parametrize("case", range(20))
+def test_random_selectors_device_vs_host(gpu, case):
+    """Random basic + advanced index tuples on a device tensor (contiguous
+    or with its last two axes stored transposed), __getitem__ and then
+    __setitem__ of a scalar, against the host path of the same API."""
+    r = rng(12000 + case)
+    shape = tuple(int(v) for v in r.choice([3, 5, 8, 13], 3))
+    a = (r.standard_normal(shape) * 10).astype(np.float32)
+    if r.random() < 0.5:
+        x = dev(a)
+    else:
+        x = dev(np.ascontiguousarray(np.swapaxes(a, 1, 2))).transpose(1, 2)
+    h = nt.Tensor(a.copy())
+    sel = _random_selector(r, shape)
+    want = h[sel].numpy()
+    got = x[sel]
+    assert got.device == nt.Device.Cuda
+    assert_bitexact(got.numpy(), want, f"case {case} getitem {sel}")
+    h[sel] = 7.5
+    x[sel] = 7.5
+    assert_bitexact(x.numpy(), h.numpy(), f"case {case} setitem {sel}")
