@@ -50,6 +50,10 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 #ifndef NT_MM_SPLITK_MAX
 #define NT_MM_SPLITK_MAX 8
 #endif
+// The split-K sum kernel is instantiated for 2, 4 and 8 slices only.
+static_assert(NT_MM_SPLITK_MAX == 1 || NT_MM_SPLITK_MAX == 2 ||
+                  NT_MM_SPLITK_MAX == 4 || NT_MM_SPLITK_MAX == 8,
+              "NT_MM_SPLITK_MAX must be 1, 2, 4 or 8");
 
 constexpr int MM_BM = 128, MM_BN = 128, MM_BK = 32, MM_THREADS = 256;
 constexpr int MM_KPAD = MM_BK + 4;  // [mn][k] row length (floats)
@@ -786,8 +790,10 @@ template <int LA, int LB> void launch_mfma(const MMArgs &a, int64_t blocks) {
             NT_SPLITK_SUM(2);
           else if (S == 4)
             NT_SPLITK_SUM(4);
-          else
+          else if (S == 8)
             NT_SPLITK_SUM(8);
+          else
+            fail(NT_ERR_RUNTIME, "matmul: no split-K sum for this slice count");
 #undef NT_SPLITK_SUM
           return;
         }

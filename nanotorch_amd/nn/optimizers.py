@@ -4,6 +4,7 @@ from __future__ import annotations
 
 from typing import Sequence
 
+import math
 import struct
 
 from .. import _kernels as K
@@ -37,11 +38,15 @@ class GradientDescent(Optimizer):
         self._lr = lr
 
     def step(self) -> None:
-        # lr as the reference's 0-d scalar tensor holds it (float32); a step
-        # size beyond float32's range takes the composition (an inf scalar)
+        # lr as the reference's 0-d scalar tensor holds it (float32).  A step
+        # size beyond float32's range (an inf scalar), a NaN, or anything that
+        # is not a plain real number (e.g. a Tensor) takes the composition,
+        # which gives what `p -= g * lr` gives for it.
         try:
             lr32 = struct.unpack("f", struct.pack("f", self._lr))[0]
-        except OverflowError:
+        except (OverflowError, struct.error, TypeError):
+            lr32 = None
+        if lr32 is not None and (math.isnan(lr32) or isinstance(self._lr, Tensor)):
             lr32 = None
         for p in self.parameters:
             if p.requires_grad:

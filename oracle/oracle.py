@@ -336,7 +336,11 @@ def mlp_step(params, x, t, acts, lr: float, parallel: bool = True, stats: dict |
     With `stats` (a dict), also stores stats["sq_sum64"], the float64 sum of
     the squared-error tensor (Y - T)**2 the loss is the mean of, and
     stats["numel"]: the loss with the reference's sequential fp32
-    summation error taken out (the backward does not depend on it)."""
+    summation error taken out (the backward does not depend on it); and,
+    per layer i, stats["grads"][i] = (W.grad, b.grad) of this step,
+    stats["layer_in"][i] = the layer's input A_i and stats["layer_dz"][i] =
+    the gradient dZ_i of its output z = A_i @ W + b, so that W.grad =
+    A_i^T @ dZ_i and b.grad = sum over rows of dZ_i."""
     mm = lambda a, b: matmul(a, b, parallel=parallel)  # noqa: E731
     hs = [x]  # layer inputs
     zs_saved = []  # saved activation outputs
@@ -371,10 +375,12 @@ def mlp_step(params, x, t, acts, lr: float, parallel: bool = True, stats: dict |
     gd = bwd_pow(gs, d, 2)
     gY = gd  # SubOp: grad for Y passes through
     grads = []
+    dzs = []
     g = gY
     for i in range(n - 1, -1, -1):
         W, b = params[i]
         hin = hs[i]
+        dzs.append(g)
         # z = (h @ W) + b: AddOp backward -> (g, unbroadcast(g, b.shape))
         gb = reduce(R_SUM, g, (0,), np.float32)
         gW = mm(hin.T, g)
@@ -390,6 +396,11 @@ def mlp_step(params, x, t, acts, lr: float, parallel: bool = True, stats: dict |
             else:
                 g = bwd_sigmoid(gh, y)
     grads.reverse()
+    dzs.reverse()
+    if stats is not None:
+        stats["grads"] = grads
+        stats["layer_in"] = hs
+        stats["layer_dz"] = dzs
     # SGD: p -= p.grad * lr  (two roundings)
     for (W, b), (gW, gb) in zip(params, grads):
         inplace(SUB, W, mul_scalar(gW, lr))

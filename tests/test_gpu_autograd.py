@@ -326,6 +326,42 @@ def test_config5_mlp_shape_scaled_vs_oracle(gpu):
         assert abs(g - w) <= 1e-4 * abs(w), (g, w)
 
 
+def _check_step0_gradients(layers, ref):
+    """Config 5's first-step W.grad (4096 sampled positions per layer) and
+    b.grad (all) against the CPU reference's (make_config5_trace.py), with
+    scale = |A|^T @ |dZ| (|dZ| summed over rows for b.grad), the size of the
+    terms each element sums.  Measured on the MI355X, |diff| / scale: W1
+    8.8e-5, W2 4.0e-5, W4 1.1e-4 at most; b1, b2, b4 3.6e-5 at most.
+
+    Layer 3's output goes through the ReLU, and wherever |z| there is below
+    the GPU-vs-reference rounding difference (~1e-5 of the matmul's scale:
+    about one element in 3e4) the two masks differ, which changes a whole
+    row's term of W3.grad / b3.grad: one such row in a column moves that
+    column by ~1/8192 of its scale.  Those layers are held in norm, where
+    the flipped rows weigh what they are (measured 1.1e-5 of |g|).  Upstream
+    of the ReLU the flips reach dZ1 and dZ2 through dZ3 @ W3^T, one term in
+    4096, which is why W1 and W2 sit near 1e-4 rather than at the single
+    matmul's ~1e-6; their per-element bound is 2e-4 of scale.  At |g| ~ 2%
+    of scale (the median here), that pins each sampled gradient to ~1%, and
+    a zero or 19%-wrong gradient fails at nearly every position.  Positions
+    whose scale is zero (units dead for the whole batch) must be exactly 0."""
+    for i, lin in enumerate(layers):
+        for name, got, want, sc, per_elem in (
+                (f"W{i + 1}", host(lin._W.grad).ravel()[ref[f"w{i}_idx"]], ref[f"gw{i}_step0"],
+                 ref[f"gw{i}_scale"], 2e-4),
+                (f"b{i + 1}", host(lin._b.grad), ref[f"gb{i}_step0"], ref[f"gb{i}_scale"], 1e-4)):
+            got = got.astype(np.float64)
+            want = want.astype(np.float64)
+            err = np.abs(got - want)
+            dead = sc == 0
+            assert (got[dead] == 0).all() and (want[dead] == 0).all(), (name, int(dead.sum()))
+            rel = float(np.linalg.norm(err) / np.linalg.norm(want))
+            assert rel <= (1e-4 if i == 2 else 1e-3), (name, rel)
+            if i != 2:
+                q = err[~dead] / sc[~dead]
+                assert (q <= per_elem).all(), (name, float(q.max()))
+
+
 def test_config5_full_size_vs_cpu_reference(gpu):
     """Config 5 at its size: batch 8192, 1024 -> 4096 (tanh) -> 4096
     (sigmoid) -> 4096 (ReLU) -> 1000, MSE, SGD lr 1e-3, 20 steps on
@@ -347,7 +383,10 @@ def test_config5_full_size_vs_cpu_reference(gpu):
     is only ~20 ulps of W (one per step), so a difference of ~1e-6 in
     fl(g * lr) can move the rounded W by one ulp in a step: the bound is
     1e-3 of the reference's update plus one ulp of W per step, per element
-    (max) and in norm (sqrt(steps) ulps, rounding flips being independent)."""
+    (max) and in norm (sqrt(steps) ulps, rounding flips being independent).
+    Those bounds barely bind on layers 1 and 2, whose whole update is a few
+    ulps, so the first step's gradients are also checked directly, before
+    any rounding of W can hide them (_check_step0_gradients)."""
     import bench
 
     with np.load(bench.C5_TRACE, allow_pickle=False) as z:
@@ -358,10 +397,12 @@ def test_config5_full_size_vs_cpu_reference(gpu):
     del x, t
     opt = nn.GradientDescent(model.parameters(), lr=bench.C5_LR)
     losses = []
-    for _ in range(len(ref["losses"])):
+    for step in range(len(ref["losses"])):
         opt.zero_grad()
         loss = nt.mean((model(X) - T) ** 2)
         loss.backward()
+        if step == 0:
+            _check_step0_gradients(layers, ref)
         opt.step()
         losses.append(float(loss.cpu().item()))
     lit = ref["losses"].astype(np.float64)
@@ -438,6 +479,25 @@ def test_sgd_step_guards_and_float64_path(gpu):
     nn.GradientDescent([p], lr=1e-3).step()
     want = p0 - g0 * np.float64(np.float32(1e-3))
     assert_bitexact(host(p), want, "sgd float64")
+
+
+def test_sgd_step_nan_and_tensor_lr_take_the_composition(gpu):
+    # A NaN step size and a 0-d Tensor step size are not float32 values the
+    # one-pass kernel takes: step() must give what p -= g * lr gives (NaN
+    # parameters; the tensor product's two roundings), not raise.
+    r = rng(seed_of("sgd-lr-forms"))
+    p0 = r.standard_normal((5, 7)).astype(np.float32)
+    g0 = r.standard_normal((5, 7)).astype(np.float32)
+    for lr in (float("nan"), nt.Tensor(np.array(0.25, np.float32), device="cuda")):
+        p = dev(p0)
+        p.enable_grad()
+        p._grad = dev(g0)
+        nn.GradientDescent([p], lr=lr).step()
+        q = dev(p0)
+        with nt.no_grad():
+            q -= dev(g0) * lr
+        assert_bitexact(host(p), host(q), f"sgd lr {lr!r}")
+    assert np.isnan(host(q)).sum() == 0  # the tensor step: finite
 
 
 _CHAIN_UNARY = {  # name: (Tensor op, oracle op, oracle backward of (g, input, output))

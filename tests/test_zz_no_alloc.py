@@ -8,6 +8,7 @@ first call's partial results in the shared static scratch array."""
 from __future__ import annotations
 
 import ctypes
+import gc
 
 import numpy as np
 import pytest
@@ -78,9 +79,18 @@ def test_noalloc_reduce_matches_nt_reduce(gpu, shape, axes):
         got = _outputs(op, kshape)
         sgot = _outputs(op, skshape)
         nt.sync()
+        # Return every cached block to HIP first: nt_reduce above has just
+        # cached partial blocks of exactly the sizes a fallback to the
+        # allocator would ask for, and such an allocation would take one
+        # and give it back, leaving both figures as they were.  With the
+        # cache empty, any block taken inside the calls ends up cached.
+        gc.collect()
+        _lib.call("nt_empty_cache")
         before = _stats()
+        assert before[1] == 0, before
         _call("nt_reduce_noalloc", op, x, axes, got, aux)
         _call("nt_reduce_noalloc", op, sx, axes, sgot, aux)
+        nt.sync()
         after = _stats()
         assert after == before, (op, before, after)
         for w, g in zip(want + swant, got + sgot):
