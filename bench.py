@@ -4,9 +4,10 @@
 
 Headline (`value`): config 2 of BASELINE.json -- the elementwise forward +
 fused backward sweep at 2^24 fp32 elements ([4096, 4096]): each of add, sub,
-mul, truediv, neg, exp, log, sqrt, pow(2.5), relu, sigmoid, tanh, forward then
-backward in accumulate mode, once on contiguous tensors and once on
-transposed (`.T`) views.  One step = one full sweep (48 kernels).  `value` is
+mul, truediv, neg, exp, log, sqrt, pow(2.5), relu, sigmoid, tanh, forward and
+backward in accumulate mode (the 12 forwards of a layout, then its 12
+backwards), once on contiguous tensors and once on transposed (`.T`) views.
+One step = one full sweep (48 kernels).  `value` is
 the sweep's algorithmic HBM bytes / its time (GB/s); inputs are resident in
 HBM before timing.  Timing uses HIP events on the library stream.
 
@@ -126,7 +127,17 @@ def ew_bytes(name: str, phase: str) -> int:
 
 class ElementwiseSweep:
     """Prepared tensors and C views for the config-2 sweep; `step()` queues
-    the 48 kernels through the C ABI with no allocation in the loop."""
+    the 48 kernels through the C ABI with no allocation in the loop.
+
+    Order within a layout: the 12 forwards, then the 12 backwards in the
+    same op order, as a training step runs every forward before any
+    backward (the reference's engine, src/nanotorch/core.py:511-526 and
+    836-872).  Between an op's forward and its backward the other 22
+    kernels of the layout move ~5 GB, so the saved output `y` a backward
+    reads (exp, sqrt, relu, sigmoid, tanh) has left the 256 MB Infinity
+    Cache and comes from HBM, as every other operand of the sweep does.
+    Queued forward-then-backward per op, those five backwards read a `y`
+    written microseconds earlier and run above the rate HBM allows."""
 
     def __init__(self, seed: int = 0) -> None:
         r = np.random.default_rng(seed)
@@ -136,6 +147,8 @@ class ElementwiseSweep:
         keep = []  # keep tensors alive
         for layout in ("contig", "transposed"):
             mk = dev if layout == "contig" else dev_T
+            fwds: list = []
+            bwds: list = []
             for name, op in BINARY_OPS:
                 a = r.standard_normal(shape).astype(np.float32)
                 b = (r.uniform(0.5, 2, shape) if name == "truediv" else r.standard_normal(shape)).astype(np.float32)
@@ -146,8 +159,8 @@ class ElementwiseSweep:
                 ga, gb = mk(r.standard_normal(shape).astype(np.float32)), mk(r.standard_normal(shape).astype(np.float32))
                 va, vb, vg, vo, vga, vgb = view(ta), view(tb), view(tg), view(out), view(ga), view(gb)
                 keep += [ta, tb, tg, out, ga, gb, va, vb, vg, vo, vga, vgb]
-                self.calls.append((name, layout, "fwd", (lib.nt_binary, (op, ctypes.byref(va), ctypes.byref(vb), ctypes.byref(vo)))))
-                self.calls.append((name, layout, "bwd", (lib.nt_binary_bwd, (
+                fwds.append((name, layout, "fwd", (lib.nt_binary, (op, ctypes.byref(va), ctypes.byref(vb), ctypes.byref(vo)))))
+                bwds.append((name, layout, "bwd", (lib.nt_binary_bwd, (
                     op, ctypes.byref(vg), ctypes.byref(va), ctypes.byref(vb),
                     ctypes.byref(vga), 1, ctypes.byref(vgb), 1))))
             for name, op, dom, saved, e in UNARY_OPS:
@@ -160,10 +173,11 @@ class ElementwiseSweep:
                 # saved tensor: the forward output (contiguous) or the input view
                 vs = vo if saved == "out" else (vx if saved == "in" else None)
                 keep += [tx, tg, out, gx, vx, vg, vo, vgx]
-                self.calls.append((name, layout, "fwd", (lib.nt_unary, (op, ctypes.byref(vx), e, ctypes.byref(vo)))))
-                self.calls.append((name, layout, "bwd", (lib.nt_unary_bwd, (
+                fwds.append((name, layout, "fwd", (lib.nt_unary, (op, ctypes.byref(vx), e, ctypes.byref(vo)))))
+                bwds.append((name, layout, "bwd", (lib.nt_unary_bwd, (
                     op, ctypes.byref(vg), ctypes.byref(vs) if vs is not None else None, e,
                     ctypes.byref(vgx), 1))))
+            self.calls += fwds + bwds
         self._keep = keep
         self.step_bytes = sum(ew_bytes(n, ph) for n, _, ph, _ in self.calls)
 
@@ -175,7 +189,20 @@ class ElementwiseSweep:
                 timer.run(f"{name}|{layout}|{phase}", lambda fn=fn, args=args: _lib.check(fn(*args)))
 
 
+def launch_stats() -> dict:
+    """nt_launch_stats: elementwise kernels queued without / with the stream
+    barrier, and barrier kernels queued before other stream work."""
+    u, o, f = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    _lib.call("nt_launch_stats", ctypes.byref(u), ctypes.byref(o), ctypes.byref(f))
+    return {"unordered": u.value, "ordered": o.value, "fences": f.value}
+
+
 def bench_elementwise(steps: int, warmup: int) -> dict:
+    """The sweep's whole-step time (events around the K steps; independent
+    kernels overlap where the library's launch window admits them), then a
+    per-kernel pass with events around each launch, which orders every
+    kernel after the one before (no overlap): the per-kernel figures and the
+    roofline come from that pass."""
     sw = ElementwiseSweep()
     for _ in range(warmup):
         sw.step()
@@ -183,11 +210,13 @@ def bench_elementwise(steps: int, warmup: int) -> dict:
     # whole-step timing: events around the K steps only
     t0, t1 = _lib.Event(), _lib.Event()
     nt.sync()
+    l0 = launch_stats()
     t0.record()
     for _ in range(steps):
         sw.step()
     t1.record()
     nt.sync()
+    l1 = launch_stats()
     total_ms = t0.elapsed_ms(t1)
     # per-kernel timing (separate pass, events around each launch)
     tm = Timer()
@@ -201,7 +230,10 @@ def bench_elementwise(steps: int, warmup: int) -> dict:
         gbs = ew_bytes(name, phase) / (avg * 1e-3) / 1e9
         per[key] = {"ms": round(avg, 5), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                     "bytes": ew_bytes(name, phase)}
-    return {"ms_per_step": total_ms / steps, "step_bytes": sw.step_bytes, "per_kernel": per}
+    launches = {k: (l1[k] - l0[k]) / steps for k in l0}
+    return {"ms_per_step": total_ms / steps, "step_bytes": sw.step_bytes, "per_kernel": per,
+            "launches_per_step": launches,
+            "sum_of_kernel_ms": round(sum(v["ms"] for v in per.values()), 5)}
 
 
 # ---------------------------------------------------- config 3: reductions
@@ -298,10 +330,14 @@ def bench_reductions(iters: int = 8) -> dict:
 # ------------------------------------------------------- config 4: matmul
 
 
-def bench_matmul(iters: int = 5) -> dict:
+MM_SHAPES = ((4096, 4096, 4096), (8192, 1024, 4096))
+MM_ITERS = 5
+
+
+def bench_matmul(iters: int = MM_ITERS) -> dict:
     r = np.random.default_rng(4)
     res = {}
-    for (M, Kd, N) in ((4096, 4096, 4096), (8192, 1024, 4096)):
+    for (M, Kd, N) in MM_SHAPES:
         A = r.standard_normal((M, Kd)).astype(np.float32)
         B = (r.standard_normal((Kd, N)) / np.sqrt(Kd)).astype(np.float32)
         G = r.standard_normal((M, N)).astype(np.float32)
@@ -918,48 +954,154 @@ def _sweep_key(name: str):
     return f"{opn}|{layout}|{'fwd' if kind.endswith('Fwd') else 'bwd'}"
 
 
+def _mm_calls():
+    """bench_matmul's calls in queue order: (M, K, N, A layout, product, is
+    the untimed first round)."""
+    out = []
+    for (M, Kd, N) in MM_SHAPES:
+        for lay in ("contig", "transposed"):
+            for it in range(MM_ITERS + 1):
+                for prod in ("fwd", "dA", "dB"):
+                    out.append((M, Kd, N, lay, prod, it == 0))
+    return out
+
+
+def _mm_dispatches(rows):
+    """Assigns matmul dispatches (dicts with Kernel_Name, in dispatch order)
+    to bench_matmul's calls: each call is one product kernel, followed by
+    the split-K sum kernel when K is split.  Yields (call, row, is_sum)."""
+    calls = _mm_calls()
+    ci = -1
+    for r in rows:
+        name = r["Kernel_Name"]
+        if "mm_" not in name:
+            continue
+        is_sum = "splitk_sum" in name
+        if not is_sum:
+            ci += 1
+        if 0 <= ci < len(calls):
+            yield calls[ci], r, is_sum
+
+
+SWEEP_TIMER_SWEEPS = 2  # bench_elementwise's per-kernel pass under PROFILE_CMDS["sweep"] (--steps 5)
+
+
+def _summarize_sweep_trace(path: str, out_md: str) -> None:
+    """Config-2 kernel times from the kernel trace: per sweep kernel, the
+    average over every dispatch (warm-up, whole-step and per-kernel passes;
+    in the whole-step passes independent kernels overlap, which stretches
+    each one's start-to-end time) and over the per-kernel pass alone, whose
+    launches are ordered one after another -- the durations bench.py's
+    per-kernel figures and roofline come from."""
+    import csv
+    rows = sorted(csv.DictReader(open(os.path.join(path, "run_kernel_trace.csv"))),
+                  key=lambda r: int(r["Dispatch_Id"]))
+    per: dict = {}
+    for r in rows:
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        key = (_short(r["Kernel_Name"]), _sweep_key(r["Kernel_Name"]) or "",
+               f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}")
+        per.setdefault(key, []).append(us)
+    total = sum(sum(v) for v in per.values())
+    with open(out_md, "w") as o:
+        o.write(f"# {PROFILE_FILES['sweep'][1]}\n\nCommand (repo root on the GPU box):\n\n"
+                f"```\n{PROFILE_CMDS['sweep']}\n```\n\n"
+                "Summarised with `python bench.py --summarize sweep gpurun_out/prof_sweep` from the "
+                "kernel trace.  `all` averages every dispatch of the kernel (2 warm-up and 5 "
+                "whole-step sweeps, where independent kernels are queued without the stream "
+                "barrier and overlap their neighbours, then the per-kernel pass); `per-kernel "
+                f"pass` averages the last {SWEEP_TIMER_SWEEPS} dispatches, bench.py's per-kernel "
+                "pass, whose events order every launch after the one before: the durations the "
+                "bench line's per-kernel figures and roofline are measured on.  "
+                "`stream_fence_kernel` is the empty barrier kernel queued before an event or a "
+                "copy while overlapped kernels may still run.\n\n"
+                "| kernel | sweep key | grid | calls | all avg us | per-kernel pass avg us | "
+                "min us | max us | share of kernel time % |\n|---|---|---|---|---|---|---|---|---|\n")
+        for (name, sk, grid), v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            tp = v[-SWEEP_TIMER_SWEEPS:] if sk else v
+            o.write(f"| `{name[:150]}` | {sk} | {grid} | {len(v)} | {sum(v) / len(v):.2f} | "
+                    f"{sum(tp) / len(tp):.2f} | {min(v):.2f} | {max(v):.2f} | "
+                    f"{100 * sum(v) / total:.2f} |\n")
+
+
+def _summarize_mm_trace(path: str, out_md: str) -> None:
+    """Config-4 kernel times per product and shape from the kernel trace
+    (one row per (shape, A layout, product): the product kernel and, with
+    split K, the sum kernel), timed rounds only, as bench_matmul reports."""
+    import csv
+    rows = sorted(csv.DictReader(open(os.path.join(path, "run_kernel_trace.csv"))),
+                  key=lambda r: int(r["Dispatch_Id"]))
+    acc: dict = {}
+    for (M, Kd, N, lay, prod, warm), r, is_sum in _mm_dispatches(rows):
+        if warm:
+            continue
+        e = acc.setdefault((M, Kd, N, lay, prod), {"main": [], "sum": [], "name": "", "grid": ""})
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if is_sum:
+            e["sum"].append(us)
+        else:
+            e["main"].append(us)
+            e["name"] = _short(r["Kernel_Name"])
+            e["grid"] = f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}"
+    with open(out_md, "w") as o:
+        o.write("# Kernel times: config-4 MatMulOp forward + dA + dB, per product and shape\n\n")
+        o.write(f"Command (repo root on the GPU box):\n\n```\n{PROFILE_CMDS['mm']}\n```\n\n")
+        o.write("Summarised with `python bench.py --summarize mm gpurun_out/prof_mm` from the "
+                "kernel trace: each dispatch is matched to bench_matmul's call sequence (per shape, "
+                "per A layout, rounds of fwd, dA = dG.B^T, dB = A^T.dG; the first round untimed), "
+                "so the two config-4 shapes get rows of their own.  `sum us` is the split-K sum "
+                "kernel where K is split; TFLOP/s = 2MNK / (product + sum).  Grid in work-items "
+                "(x by split-K slices).\n\n")
+        o.write("| shape MxKxN | A | product | kernel | grid | n | product us | sum us | TFLOP/s | frac of 157.3 |\n"
+                "|---|---|---|---|---|---|---|---|---|---|\n")
+        for (M, Kd, N, lay, prod), e in acc.items():
+            mu = sum(e["main"]) / len(e["main"])
+            su = sum(e["sum"]) / len(e["sum"]) if e["sum"] else 0.0
+            m_, k_, n_ = {"fwd": (M, Kd, N), "dA": (M, N, Kd), "dB": (Kd, M, N)}[prod]
+            tf = 2.0 * m_ * n_ * k_ / ((mu + su) * 1e-6) / 1e12
+            o.write(f"| {M}x{Kd}x{N} | {lay} | {prod} | `{e['name'][:60]}` | {e['grid']} | {len(e['main'])} | "
+                    f"{mu:.1f} | {su:.1f} | {tf:.1f} | {tf / FP32_MFMA_PEAK_TFLOPS:.3f} |\n")
+
+
 def _summarize_mm_pmc(path: str, out_md: str) -> None:
-    """MFMA-pipe utilisation per matmul kernel and grid: busy cycles of the
-    matrix pipe summed over the 1024 SIMDs, over SIMDs x duration x clock."""
+    """MFMA-pipe utilisation per product and shape: busy cycles of the
+    matrix pipe summed over the 1024 SIMDs, over SIMDs x duration x clock,
+    each dispatch matched to bench_matmul's call sequence (_mm_dispatches)."""
     import csv
     simds, clock_ghz = 256 * 4, 2.4
-    per: dict[tuple, dict] = {}
+    disp: dict[int, dict] = {}
     for r in csv.DictReader(open(os.path.join(path, "run_counter_collection.csv"))):
-        if "mfma" not in r["Kernel_Name"]:
-            continue
-        key = (_short(r["Kernel_Name"]), int(r["Grid_Size"]))
-        d = per.setdefault(key, {"dispatch": {}})
-        disp = d["dispatch"].setdefault(r["Dispatch_Id"], {
+        d = disp.setdefault(int(r["Dispatch_Id"]), {
+            "Kernel_Name": r["Kernel_Name"], "grid": r["Grid_Size"],
             "dur_ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
-        disp[r["Counter_Name"]] = float(r["Counter_Value"])
-    rows = []
-    for (name, grid), d in sorted(per.items()):
-        ds = list(d["dispatch"].values())
-        avg = lambda k: sum(x.get(k, 0.0) for x in ds) / len(ds)  # noqa: E731
-        dur = avg("dur_ns")
-        busy = avg("SQ_VALU_MFMA_BUSY_CYCLES")
-        util = busy / (simds * dur * clock_ghz) if dur else 0.0
-        rows.append((name, grid, len(ds), dur / 1e3, avg("SQ_INSTS_MFMA"), busy, util,
-                     avg("SQ_WAIT_INST_LDS") / max(avg("SQ_WAVE_CYCLES"), 1.0),
-                     avg("SQ_LDS_BANK_CONFLICT")))
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+    rows = [disp[k] for k in sorted(disp)]
+    per: dict = {}
+    for (M, Kd, N, lay, prod, warm), d, is_sum in _mm_dispatches(rows):
+        if warm or is_sum:
+            continue
+        per.setdefault((M, Kd, N, lay, prod), []).append(d)
     with open(out_md, "w") as o:
-        o.write("# MFMA-pipe utilisation: config-4 matmul kernels\n\n")
+        o.write("# MFMA-pipe utilisation: config-4 matmul kernels, per product and shape\n\n")
         o.write(f"Command (repo root on the GPU box):\n\n```\n{PROFILE_CMDS['mm_pmc']}\n```\n\n")
-        o.write("Summarised with `python bench.py --summarize mm_pmc gpurun_out/prof_mm_pmc`. "
+        o.write("Summarised with `python bench.py --summarize mm_pmc gpurun_out/prof_mm_pmc`; "
+                "each dispatch is matched to bench_matmul's call sequence, timed rounds only, "
+                "the product kernel alone (a split-K sum kernel has no MFMA). "
                 "Utilisation = SQ_VALU_MFMA_BUSY_CYCLES (summed over the 1024 SIMDs) / "
                 "(1024 x kernel duration x 2.4 GHz); each v_mfma_f32_32x32x2_f32 keeps the "
                 "pipe busy 64 cycles, so this equals achieved / peak FLOP rate at 2.4 GHz. "
-                "Grid in work-items: the 128x128 kernel (`mm_f32_mfma_dl_kernel`, 256 per "
-                "tile) has 65536 for a 1024x4096 output and 131072 for 8192x1024; the wide "
-                "kernel (`mm_f32_mfma_wide_kernel`, 512 per 256x256 tile) has 131072 for "
-                "4096x4096 and 262144 for 8192x4096. "
                 "Durations are from this (counter-collecting) run.\n\n")
-        o.write("| kernel | grid | dispatches | avg us | MFMA instr | MFMA busy cycles | "
-                "MFMA util | LDS-wait / wave cycles | LDS bank conflicts |\n"
-                "|---|---|---|---|---|---|---|---|---|\n")
-        for name, grid, n, us, inst, busy, util, lw, bc in rows:
-            o.write(f"| `{name}` | {grid} | {n} | {us:.1f} | {inst:.0f} | {busy:.3g} | "
-                    f"{util:.3f} | {lw:.3f} | {bc:.0f} |\n")
+        o.write("| shape MxKxN | A | product | kernel | grid | n | avg us | MFMA instr | MFMA util | "
+                "LDS-wait / wave cycles | LDS bank conflicts |\n"
+                "|---|---|---|---|---|---|---|---|---|---|---|\n")
+        for (M, Kd, N, lay, prod), ds in per.items():
+            avg = lambda k: sum(x.get(k, 0.0) for x in ds) / len(ds)  # noqa: E731
+            dur = avg("dur_ns")
+            util = avg("SQ_VALU_MFMA_BUSY_CYCLES") / (simds * dur * clock_ghz) if dur else 0.0
+            lw = avg("SQ_WAIT_INST_LDS") / max(avg("SQ_WAVE_CYCLES"), 1.0)
+            o.write(f"| {M}x{Kd}x{N} | {lay} | {prod} | `{_short(ds[0]['Kernel_Name'])[:60]}` | "
+                    f"{ds[0]['grid']} | {len(ds)} | {dur / 1e3:.1f} | {avg('SQ_INSTS_MFMA'):.0f} | "
+                    f"{util:.3f} | {lw:.3f} | {avg('SQ_LDS_BANK_CONFLICT'):.0f} |\n")
 
 
 def _load_pmc(path: str) -> dict:
@@ -1095,6 +1237,12 @@ def summarize(kind: str, dirs: list[str]) -> None:
     if kind == "mlp_bytes":
         _summarize_bytes("mlp", dirs, os.path.join(prof, "mlp_config5_hbm_traffic.md"),
                          "HBM traffic per launch: config-5 MLP step kernels", lambda n, g: "")
+        return
+    if kind == "sweep":
+        _summarize_sweep_trace(dirs[0], os.path.join(prof, PROFILE_FILES["sweep"][0]))
+        return
+    if kind == "mm":
+        _summarize_mm_trace(dirs[0], os.path.join(prof, PROFILE_FILES["mm"][0]))
         return
     if kind in PROFILE_FILES:
         fname, title = PROFILE_FILES[kind]
@@ -1250,6 +1398,10 @@ def main() -> int:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
                      "traffic": traffic, "bytes_per_launch": dom["bytes"]},
         "sweep_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        # kernels of a step queued without / with the stream barrier (the
+        # launch window), and the per-kernel pass's sum of kernel times
+        "launches_per_step": ew["launches_per_step"],
+        "sum_of_kernel_ms": ew["sum_of_kernel_ms"],
         "parts": {"elementwise_per_kernel": ew["per_kernel"]},
     }
     copy_ref = bench_copy_reference()

@@ -21,7 +21,12 @@
  *    std::invalid_argument through pybind11).
  *  - All device work is ordered on one HIP stream owned by the library.
  *    Calls return once work is queued; nt_sync() and the device-to-host copy
- *    wait for it.  Single-threaded callers only.
+ *    wait for it.
+ *  - Any host thread may call any entry point.  Calls are serialised by one
+ *    library-wide (recursive) lock, and the caching allocator has a lock of
+ *    its own, so concurrent callers queue their work on the stream one call
+ *    at a time.  This is the guarantee the reference's binding gets from the
+ *    Python GIL.
  */
 #ifndef NT_H_
 #define NT_H_
@@ -343,6 +348,15 @@ int nt_event_create(void **ev);
 int nt_event_record(void *ev);
 int nt_event_elapsed_ms(void *start, void *end, float *ms);
 int nt_event_destroy(void *ev);
+
+/* No counterpart in the reference (the reference launches every kernel in
+ * stream order): counts, since the library initialised, of elementwise
+ * kernels queued without the stream barrier (hipExtAnyOrderLaunch; allowed
+ * only between kernels that touch no common bytes, see launch_window.h),
+ * elementwise kernels queued with it, and the empty barrier kernels queued
+ * before other stream work while such kernels could still be running.  A
+ * diagnostic for tests and benchmarks; any pointer may be NULL. */
+int nt_launch_stats(uint64_t *unordered, uint64_t *ordered, uint64_t *fences);
 
 #ifdef __cplusplus
 }

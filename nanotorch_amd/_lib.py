@@ -97,6 +97,7 @@ _SIGNATURES = {
     "nt_event_record": (c_int, [c_void_p]),
     "nt_event_elapsed_ms": (c_int, [c_void_p, c_void_p, POINTER(c_float)]),
     "nt_event_destroy": (c_int, [c_void_p]),
+    "nt_launch_stats": (c_int, [POINTER(c_uint64), POINTER(c_uint64), POINTER(c_uint64)]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -29,98 +29,9 @@
 // as the reference does with its fp32 exponent tensor.  Accumulate mode is
 // `old + term` with one rounding, the reference's add_inplace
 // (src/cpp/ops/inplace_ops.cu:75).
-#include "ew_engine.h"
-#include "nt_math.h"
+#include "ew_ops.h"
 
 namespace nt {
-
-template <int OP> constexpr bool unary_uses_saved() { return OP != NT_NEG; }
-
-template <int OP, class T, bool ACC> struct UnaryBwd {
-  T e;   // pow exponent (already rounded as the reference's fp32 tensor)
-  T em1; // e - 1 formed in fp32
-  PowPlan plan; // evaluation plan for pow(x, em1)
-  static constexpr bool S = unary_uses_saved<OP>();
-  static constexpr int NI = 1 + (S ? 1 : 0) + (ACC ? 1 : 0);
-  __device__ __forceinline__ void operator()(const T (&x)[NI],
-                                             T (&y)[1]) const {
-    const T g = x[0];
-    const T s = S ? x[1] : T(0);
-    T t;
-    if constexpr (OP == NT_NEG)
-      t = g * T(-1);
-    else if constexpr (OP == NT_EXP)
-      t = g * s;
-    else if constexpr (OP == NT_LOG)
-      t = g * (T(1) / s);
-    else if constexpr (OP == NT_SQRT)
-      t = (g * T(0.5)) * (T(1) / s);
-    else if constexpr (OP == NT_TANH)
-      t = g * (T(1) - s * s);
-    else if constexpr (OP == NT_SIGMOID)
-      t = (g * s) * (T(1) - s);
-    else if constexpr (OP == NT_RELU)
-      t = g * (s > T(0) ? T(1) : T(0));
-    else
-      t = (g * e) * pow_planned(s, em1, plan);
-    if constexpr (ACC)
-      y[0] = x[NI - 1] + t;
-    else
-      y[0] = t;
-  }
-};
-
-// Gradients of a binary op.  NA / NB: which gradients are produced; AA / AB:
-// accumulate into them.  Inputs, in order: g, a (if read), b (if read),
-// ga_old (if NA && AA), gb_old (if NB && AB).
-template <int OP, class T, bool NA, bool NB, bool AA, bool AB>
-struct BinaryBwd {
-  static constexpr bool UA = (OP == NT_MUL || OP == NT_DIV) && NB;
-  static constexpr bool UB =
-      (OP == NT_MUL && NA) || (OP == NT_DIV && (NA || NB));
-  static constexpr int IA = 1;
-  static constexpr int IB = 1 + (UA ? 1 : 0);
-  static constexpr int IGA = IB + (UB ? 1 : 0);
-  static constexpr int IGB = IGA + ((NA && AA) ? 1 : 0);
-  static constexpr int NI = IGB + ((NB && AB) ? 1 : 0);
-  static constexpr int NO = (NA ? 1 : 0) + (NB ? 1 : 0);
-  __device__ __forceinline__ void operator()(const T (&x)[NI],
-                                             T (&y)[NO]) const {
-    const T g = x[0];
-    const T a = UA ? x[IA] : T(0);
-    const T b = UB ? x[IB] : T(0);
-    T ta = T(0), tb = T(0);
-    if constexpr (OP == NT_ADD) {
-      ta = g;
-      tb = g;
-    } else if constexpr (OP == NT_SUB) {
-      ta = g;
-      tb = g * T(-1);
-    } else if constexpr (OP == NT_MUL) {
-      ta = b * g;
-      tb = a * g;
-    } else {
-      if constexpr (NA)
-        ta = g / b;
-      if constexpr (NB)
-        tb = ((-a) / (b * b)) * g;
-    }
-    int o = 0;
-    if constexpr (NA) {
-      if constexpr (AA)
-        y[o] = x[IGA] + ta;
-      else
-        y[o] = ta;
-      ++o;
-    }
-    if constexpr (NB) {
-      if constexpr (AB)
-        y[o] = x[IGB] + tb;
-      else
-        y[o] = tb;
-    }
-  }
-};
 
 namespace {
 
@@ -221,7 +132,7 @@ extern "C" {
 
 int nt_unary_bwd(int32_t op, const nt_view *g, const nt_view *saved,
                  double scalar, const nt_view *gx, int32_t accumulate) {
-  return guard([&] {
+  return guard_ew([&] {
     check_view(g, "unary_bwd");
     check_view(gx, "unary_bwd");
     require_same_shape(g, gx, "unary_bwd");
@@ -259,7 +170,7 @@ int nt_unary_bwd(int32_t op, const nt_view *g, const nt_view *saved,
 int nt_binary_bwd(int32_t op, const nt_view *g, const nt_view *a,
                   const nt_view *b, const nt_view *ga, int32_t acc_a,
                   const nt_view *gb, int32_t acc_b) {
-  return guard([&] {
+  return guard_ew([&] {
     check_view(g, "binary_bwd");
     if (!ga && !gb)
       return;
@@ -295,7 +206,7 @@ int nt_binary_bwd(int32_t op, const nt_view *g, const nt_view *a,
 }
 
 int nt_sgd_step(const nt_view *p, const nt_view *g, double lr) {
-  return guard([&] {
+  return guard_ew([&] {
     check_view(p, "sgd_step");
     check_view(g, "sgd_step");
     require_same_shape(p, g, "sgd_step");

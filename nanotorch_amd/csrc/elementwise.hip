@@ -11,100 +11,9 @@
 // fp32 division and square root are correctly rounded
 // (-fhip-fp32-correctly-rounded-divide-sqrt) and nothing is contracted into
 // FMA (-ffp-contract=off), so +,-,*,/,sqrt match the host bit for bit.
-#include "ew_engine.h"
-#include "nt_math.h"
+#include "ew_ops.h"
 
 namespace nt {
-
-// --------------------------------------------------------- device math
-
-__device__ __forceinline__ float d_exp(float a) { return expf(a); }
-__device__ __forceinline__ double d_exp(double a) { return exp(a); }
-__device__ __forceinline__ float d_log(float a) { return logf(a); }
-__device__ __forceinline__ double d_log(double a) { return log(a); }
-__device__ __forceinline__ float d_sqrt(float a) { return sqrtf(a); }
-__device__ __forceinline__ double d_sqrt(double a) { return sqrt(a); }
-__device__ __forceinline__ float d_tanh(float a) { return tanhf(a); }
-__device__ __forceinline__ double d_tanh(double a) { return tanh(a); }
-
-// Square-and-multiply for integer dtypes (reference: int_pow,
-// src/cpp/ops/unary_ops.cu:40-49).
-template <class T> __device__ __forceinline__ T int_pow(T a, T n) {
-  T r = 1;
-  while (n > 0) {
-    if (n & 1)
-      r *= a;
-    a *= a;
-    n >>= 1;
-  }
-  return r;
-}
-
-// ------------------------------------------------------------ functors
-
-template <int OP, class T> struct UnaryFwd {
-  T e; // exponent for NT_POW, as the reference's value.item<T>()
-  PowPlan plan;
-  __device__ __forceinline__ void operator()(const T (&x)[1], T (&y)[1]) const {
-    const T a = x[0];
-    if constexpr (OP == NT_EXP)
-      y[0] = d_exp(a);
-    else if constexpr (OP == NT_LOG)
-      y[0] = d_log(a);
-    else if constexpr (OP == NT_NEG)
-      y[0] = -a;
-    else if constexpr (OP == NT_RELU)
-      y[0] = (a >= 0) ? a : T(0);
-    else if constexpr (OP == NT_SQRT)
-      y[0] = d_sqrt(a);
-    else if constexpr (OP == NT_TANH)
-      y[0] = d_tanh(a);
-    else if constexpr (OP == NT_SIGMOID)
-      y[0] = T(1) / (T(1) + d_exp(-a));
-    else if constexpr (OP == NT_POW) {
-      if constexpr (std::is_integral_v<T>)
-        y[0] = int_pow(a, e);
-      else
-        y[0] = pow_planned(a, e, plan);
-    }
-  }
-};
-
-template <int OP, class T> struct BinaryFwd {
-  __device__ __forceinline__ void operator()(const T (&x)[2], T (&y)[1]) const {
-    const T a = x[0], b = x[1];
-    if constexpr (OP == NT_ADD)
-      y[0] = a + b;
-    else if constexpr (OP == NT_SUB)
-      y[0] = a - b;
-    else if constexpr (OP == NT_MUL)
-      y[0] = a * b;
-    else if constexpr (OP == NT_DIV)
-      y[0] = a / b;
-  }
-};
-
-template <int OP, class T> struct CompareFwd {
-  __device__ __forceinline__ void operator()(const T (&x)[2],
-                                             bool (&y)[1]) const {
-    if constexpr (OP == NT_EQ)
-      y[0] = x[0] == x[1];
-    else if constexpr (OP == NT_GT)
-      y[0] = x[0] > x[1];
-    else
-      y[0] = x[0] >= x[1];
-  }
-};
-
-template <class TI, class TO> struct CastOp {
-  __device__ __forceinline__ void operator()(const TI (&x)[1],
-                                             TO (&y)[1]) const {
-    if constexpr (std::is_same_v<TO, bool>)
-      y[0] = (x[0] != TI(0));
-    else
-      y[0] = static_cast<TO>(x[0]);
-  }
-};
 
 // ------------------------------------------------------------ host side
 
@@ -211,7 +120,7 @@ using namespace nt;
 extern "C" {
 
 int nt_copy(const nt_view *src, const nt_view *dst) {
-  return guard([&] {
+  return guard_ew([&] {
     check_view(src, "copy");
     check_view(dst, "copy");
     require_same_shape(src, dst, "copy");
@@ -226,7 +135,7 @@ int nt_copy(const nt_view *src, const nt_view *dst) {
 }
 
 int nt_unary(int32_t op, const nt_view *x, double scalar, const nt_view *out) {
-  return guard([&] {
+  return guard_ew([&] {
     check_view(x, "unary");
     check_view(out, "unary");
     require_same_shape(x, out, "unary");
@@ -255,11 +164,11 @@ int nt_unary(int32_t op, const nt_view *x, double scalar, const nt_view *out) {
 
 int nt_binary(int32_t op, const nt_view *a, const nt_view *b,
               const nt_view *out) {
-  return guard([&] { binary_dispatch(op, a, b, out, "_dispatch_binary"); });
+  return guard_ew([&] { binary_dispatch(op, a, b, out, "_dispatch_binary"); });
 }
 
 int nt_inplace(int32_t op, const nt_view *out, const nt_view *other) {
-  return guard([&] {
+  return guard_ew([&] {
     check_view(out, "_dispatch_inplace_apply");
     check_view(other, "_dispatch_inplace_apply");
     require_same_dtype(out, other, "_dispatch_inplace_apply");

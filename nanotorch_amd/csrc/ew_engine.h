@@ -9,8 +9,8 @@
 //               I/O with the (row, column) of each vector from one
 //               multiply-high division.
 //  * tile2d  -- after merging dims, the iteration space is 2-D.  One tile
-//               per workgroup (64x64; fp32 also 128x64 and 64x128, chosen
-//               by the streams in each layout); operands whose rows are
+//               per workgroup (64x64; fp32 also 64x128, 128x128 and 32x256,
+//               chosen by the streams in each layout); operands whose rows are
 //               contiguous are read straight; operands contiguous along the
 //               other axis (e.g. `x.T`) are staged through a padded LDS tile
 //               so both the global read and the global write stay
@@ -34,6 +34,9 @@
 #pragma once
 
 #include <algorithm>
+#include <type_traits>
+
+#include <hip/hip_ext.h>
 
 #include "nt_internal.h"
 
@@ -783,6 +786,44 @@ __global__ __launch_bounds__(EW_THREADS) void ew_generic_kernel(
 
 // ---------------------------------------------------------------- launcher
 
+// Queues kernel<<<grid, block, 0, s>>>(args...), without the stream barrier
+// when flags holds hipExtAnyOrderLaunch (ew_launch_flags).
+template <class... KA>
+void ew_launch(void (*kernel)(KA...), dim3 grid, dim3 block, hipStream_t s,
+               uint32_t flags, std::type_identity_t<KA>... args) {
+  if (flags == 0) {
+    kernel<<<grid, block, 0, s>>>(args...);
+    NT_LAUNCH_CHECK();
+    return;
+  }
+  void *ptrs[] = {static_cast<void *>(&args)...};
+  NT_HIP_CHECK(hipExtLaunchKernel(reinterpret_cast<const void *>(kernel), grid,
+                                  block, ptrs, 0, s, nullptr, nullptr,
+                                  int(flags)));
+}
+
+// Bytes [lo, hi) a view can touch (strides are never negative).
+inline ByteRange view_bytes(const nt_view *v) {
+  const int64_t es = int64_t(dtype_size(v->dtype));
+  int64_t last = 0;
+  for (int d = 0; d < v->ndim; ++d)
+    last += (v->shape[d] - 1) * v->strides[d];
+  ByteRange r;
+  r.lo = reinterpret_cast<uintptr_t>(v->data) + uintptr_t(v->offset * es);
+  r.hi = r.lo + uintptr_t((last + 1) * es);
+  return r;
+}
+
+// A functor may declare `static constexpr bool heavy = true` when its
+// arithmetic per element is long enough (tanh, sigmoid) to change which
+// transposed-tile layout is fastest.
+template <class F> constexpr bool ew_heavy() {
+  if constexpr (requires { F::heavy; })
+    return F::heavy;
+  else
+    return false;
+}
+
 template <class T> constexpr int ew_vec() {
   return sizeof(T) >= 16 ? 1 : int(16 / sizeof(T));
 }
@@ -799,6 +840,16 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
   const int64_t n = numel(outs[0]);
   if (n == 0)
     return;
+  // Barrier or not (launch_window.h): every operand's bytes.
+  uint32_t flags;
+  {
+    ByteRange rd[NI > 0 ? NI : 1], wr[NO];
+    for (int k = 0; k < NI; ++k)
+      rd[k] = view_bytes(ins[k]);
+    for (int m = 0; m < NO; ++m)
+      wr[m] = view_bytes(outs[m]);
+    flags = ew_launch_flags(rd, NI, wr, NO);
+  }
 
   PtrPack<const TI, NI> pin{};
   PtrPack<TO, NO> pout{};
@@ -865,14 +916,14 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
           1, (cv + FLAT_THREADS * UNROLL - 1) / (FLAT_THREADS * UNROLL));
       const dim3 grid{unsigned(blocks), 1u, 1u};
       if (aligned && ntl)
-        ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, true, F>
-            <<<grid, FLAT_THREADS, 0, s>>>(cin, smask, cout, cv, cn, f);
+        ew_launch(ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, true, F>, grid,
+                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, f);
       else if (aligned)
-        ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, false, F>
-            <<<grid, FLAT_THREADS, 0, s>>>(cin, smask, cout, cv, cn, f);
+        ew_launch(ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, false, F>, grid,
+                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, f);
       else
-        ew_flat_kernel<TI, TO, NI, NO, 1, UNROLL, false, F>
-            <<<grid, FLAT_THREADS, 0, s>>>(cin, smask, cout, cv, cn, f);
+        ew_launch(ew_flat_kernel<TI, TO, NI, NO, 1, UNROLL, false, F>, grid,
+                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, f);
       NT_LAUNCH_CHECK();
       v0 += cv;
     } while (v0 < nvec);
@@ -916,21 +967,21 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       const dim3 grid{unsigned(blocks), 1u, 1u};
       const FastDivU32 fdc{uint32_t(C)};
       if (grouped && ntl)
-        ew_rows_kernel<TI, TO, NI, NO, VBIG, RR, true, F>
-            <<<grid, NT_ROWS_THREADS, 0, s>>>(pin, sm, rb, cb, sin, pout,
-                                              uint32_t(nvec), fdc, uint32_t(C), f);
+        ew_launch(ew_rows_kernel<TI, TO, NI, NO, VBIG, RR, true, F>, grid,
+                  NT_ROWS_THREADS, s, flags, pin, sm, rb, cb, sin, pout,
+                  uint32_t(nvec), fdc, uint32_t(C), f);
       else if (grouped)
-        ew_rows_kernel<TI, TO, NI, NO, VBIG, RR, false, F>
-            <<<grid, NT_ROWS_THREADS, 0, s>>>(pin, sm, rb, cb, sin, pout,
-                                              uint32_t(nvec), fdc, uint32_t(C), f);
+        ew_launch(ew_rows_kernel<TI, TO, NI, NO, VBIG, RR, false, F>, grid,
+                  NT_ROWS_THREADS, s, flags, pin, sm, rb, cb, sin, pout,
+                  uint32_t(nvec), fdc, uint32_t(C), f);
       else if (ntl)
-        ew_rows_kernel<TI, TO, NI, NO, VBIG, 1, true, F>
-            <<<grid, NT_ROWS_THREADS, 0, s>>>(pin, sm, rb, cb, sin, pout,
-                                              uint32_t(nvec), fdc, uint32_t(C), f);
+        ew_launch(ew_rows_kernel<TI, TO, NI, NO, VBIG, 1, true, F>, grid,
+                  NT_ROWS_THREADS, s, flags, pin, sm, rb, cb, sin, pout,
+                  uint32_t(nvec), fdc, uint32_t(C), f);
       else
-        ew_rows_kernel<TI, TO, NI, NO, VBIG, 1, false, F>
-            <<<grid, NT_ROWS_THREADS, 0, s>>>(pin, sm, rb, cb, sin, pout,
-                                              uint32_t(nvec), fdc, uint32_t(C), f);
+        ew_launch(ew_rows_kernel<TI, TO, NI, NO, VBIG, 1, false, F>, grid,
+                  NT_ROWS_THREADS, s, flags, pin, sm, rb, cb, sin, pout,
+                  uint32_t(nvec), fdc, uint32_t(C), f);
       NT_LAUNCH_CHECK();
       return;
     }
@@ -944,16 +995,24 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
                     int64_t nb, const std::array<int64_t, NT> &bst) -> bool {
     // Elements are independent, so the tile may walk the transposed index
     // space.  Column-major operands go through the LDS exchange; pick the
-    // orientation in which that costs less, an exchanged output counting
-    // as three exchanged inputs (measured: two `.T` inputs and a row-major
-    // output beat two row-major inputs and a `.T` output).  E.g. a backward
-    // whose saved tensors and gradients are `.T` views exchanges only the
-    // upstream gradient instead of four inputs and two outputs.
-    constexpr int OUT_COST = 3;
+    // orientation in which that costs less.  An exchanged input costs two,
+    // an exchanged output one (ties keep the orientation): measured in the
+    // [4096, 4096] sweep, with each transposed kernel's time taken inside
+    // the sweep, the binary forwards of two `.T` inputs run 6% faster
+    // exchanging their output, the unary forwards 1-3%, and the backward of
+    // an op with a saved output 3-7% faster exchanging its `.T` gradient
+    // (read and written) than its upstream gradient and saved output.  A
+    // backward whose saved tensors and gradients are `.T` views still
+    // exchanges only the upstream gradient.  Functors marked heavy
+    // (ew_heavy: tanh, sigmoid) keep the older weights, an exchanged output
+    // costing three inputs, under which they exchange their input and
+    // compute after the exchange: in that sweep their forwards ran 3-10%
+    // slower exchanging the output.
+    const int IN_COST = ew_heavy<F>() ? 1 : 2, OUT_COST = ew_heavy<F>() ? 3 : 1;
     int cost_keep = 0, cost_swap = 0;
     for (int k = 0; k < NT; ++k) {
       const int64_t sr = st[k][0], sc = st[k][1];
-      const int wgt = k < NI ? 1 : OUT_COST;
+      const int wgt = k < NI ? IN_COST : OUT_COST;
       if (sc == 1 && sr != 0) // row-major now, exchanged after a swap
         cost_swap += wgt;
       else if (sr == 1 && sc != 0) // column-major now
@@ -1012,36 +1071,46 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       const dim3 grid{unsigned(blocks), 1u, 1u};
       const FastDivU32 tb(uint32_t(tr_n * tc_n));
       if (ntl)
-        ew_tile4_kernel<TI, TO, NI, NO, true, TR, TC, F>
-            <<<grid, unsigned(NTH), 0, s>>>(pin, sin, row_in, col_in, bcol_in,
-                                            pout, sout, row_out, col_out, R, C,
-                                            tc_n, tb, bs, f);
+        ew_launch(ew_tile4_kernel<TI, TO, NI, NO, true, TR, TC, F>, grid,
+                  unsigned(NTH), s, flags, pin, sin, row_in, col_in, bcol_in,
+                  pout, sout, row_out, col_out, R, C, tc_n, tb, bs, f);
       else
-        ew_tile4_kernel<TI, TO, NI, NO, false, TR, TC, F>
-            <<<grid, unsigned(NTH), 0, s>>>(pin, sin, row_in, col_in, bcol_in,
-                                            pout, sout, row_out, col_out, R, C,
-                                            tc_n, tb, bs, f);
+        ew_launch(ew_tile4_kernel<TI, TO, NI, NO, false, TR, TC, F>, grid,
+                  unsigned(NTH), s, flags, pin, sin, row_in, col_in, bcol_in,
+                  pout, sout, row_out, col_out, R, C, tc_n, tb, bs, f);
       NT_LAUNCH_CHECK();
       return true;
     };
     if (vec4) {
       // Tile shape by the streams in each layout, fp32 only (other types
-      // keep 64 x 64 and one instantiation).  Measured on the [4096, 4096]
-      // sweep, alternating with 64 x 64 for every kernel on one MI355X: one
-      // exchanged stream and at least three row-layout streams (the add /
-      // sub / mul backwards, which exchange only the upstream gradient)
-      // +4-6% with 128 x 64 (512-byte exchanged segments); one exchanged
-      // stream and fewer row-layout ones (the unary forwards, the neg
-      // backward) +1.5-9% with 64 x 128, pow -1%; two or more exchanged
-      // streams (binary forwards, unary backwards) were best at 64 x 64
-      // (the whole sweep 0.2 / 0.7 / 2.3% slower with 64 x 128, 128 x 64 or
-      // 128 x 128 for them).  Whole sweep +0.8%.
+      // keep 64 x 64 and one instantiation).  Chosen from each transposed
+      // kernel of the [4096, 4096] sweep timed inside the sweep (the kernels
+      // before and after it running as usual) in both orientations at
+      // 64x64, 64x128, 128x64, 32x128, 16x256, 32x256, 64x256 and 128x128:
+      //  * one exchanged stream and three or more straight ones (the binary
+      //    backwards and the backwards of ops with a saved input, which
+      //    exchange the upstream gradient): 32 x 256, i.e. the straight
+      //    streams read 1-KB runs (1-2% faster than 128 x 64, 16 x 256 and
+      //    64 x 256 within 1% of it, 16 x 512 slower);
+      //  * one exchanged stream and at most two straight ones (forwards
+      //    exchanging their output, the neg backward): 128 x 128 with 1024
+      //    work-items (2-6% faster than 64 x 128 / 64 x 64), except for
+      //    heavy functors, whose two resident workgroups per CU then wait on
+      //    each other's compute (tanh / sigmoid forwards 10% slower): they
+      //    keep 64 x 128;
+      //  * two exchanged streams (the backward of an op with a saved output,
+      //    exchanging its `.T` gradient in and out): 64 x 128;
+      //  * more: 64 x 64.
+      // Whole sweep 2% faster than the previous 128 x 64 / 64 x 128 / 64 x 64
+      // rule.
       if constexpr (std::is_same_v<TI, float> && std::is_same_v<TO, float>) {
         const int n_col = __builtin_popcount(col_in) + __builtin_popcount(col_out);
         const int n_row = __builtin_popcount(row_in) + __builtin_popcount(row_out);
         if (n_col == 1 && n_row >= 3)
-          return tile4.template operator()<128, 64>();
-        if (n_col == 1)
+          return tile4.template operator()<32, 256>();
+        if (n_col == 1 && !ew_heavy<F>())
+          return tile4.template operator()<128, 128>();
+        if (n_col <= 2)
           return tile4.template operator()<64, 128>();
         return tile4.template operator()<64, 64>();
       } else {
@@ -1054,8 +1123,8 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
     const int64_t blocks = tiles_r * tiles_c;
     if (nb == 1 && blocks * EW_THREADS < (int64_t(1) << 32)) {
       const dim3 grid{unsigned(blocks), 1u, 1u};
-      ew_tile_kernel<TI, TO, NI, NO, F><<<grid, EW_THREADS, 0, s>>>(
-          pin, sin, col_in, pout, sout, col_out, R, C, tiles_c, f);
+      ew_launch(ew_tile_kernel<TI, TO, NI, NO, F>, grid, EW_THREADS, s, flags,
+                pin, sin, col_in, pout, sout, col_out, R, C, tiles_c, f);
       NT_LAUNCH_CHECK();
       return true;
     }
@@ -1107,13 +1176,13 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
   const int64_t blocks =
       std::max<int64_t>(1, std::min<int64_t>(want, int64_t(1) << 20));
   if (idx32)
-    ew_generic_kernel<TI, TO, NI, NO, true, F>
-        <<<dim3(unsigned(blocks)), EW_THREADS, 0, s>>>(pin, pout, st, sh, n,
-                                                        f);
+    ew_launch(ew_generic_kernel<TI, TO, NI, NO, true, F>,
+              dim3(unsigned(blocks)), EW_THREADS, s, flags, pin, pout, st, sh,
+              n, f);
   else
-    ew_generic_kernel<TI, TO, NI, NO, false, F>
-        <<<dim3(unsigned(blocks)), EW_THREADS, 0, s>>>(pin, pout, st, sh, n,
-                                                        f);
+    ew_launch(ew_generic_kernel<TI, TO, NI, NO, false, F>,
+              dim3(unsigned(blocks)), EW_THREADS, s, flags, pin, pout, st, sh,
+              n, f);
   NT_LAUNCH_CHECK();
 }
 

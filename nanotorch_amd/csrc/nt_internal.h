@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "launch_window.h"
 #include "nt.h"
 
 namespace nt {
@@ -85,12 +86,54 @@ private:
 // its own lock as well (caching_allocator.h).
 std::recursive_mutex &api_mutex();
 
+// Launch flags for an elementwise-engine kernel that reads `reads` and
+// writes `writes` (byte ranges): hipExtAnyOrderLaunch when the launch
+// window (launch_window.h) admits it, i.e. the calling entry point is an
+// elementwise one (WindowScope) and the kernel has no hazard with the
+// kernels queued since the last barrier launch; else 0.  NT_OVERLAP=0 turns
+// the overlap off.
+uint32_t ew_launch_flags(const ByteRange *reads, int nr,
+                         const ByteRange *writes, int nw);
+// Closes the launch window: when a kernel of it went without the barrier,
+// queues an empty barrier kernel, so that whatever is queued next (a copy,
+// an event, a synchronisation, any other kernel) starts after every earlier
+// kernel has finished.
+void stream_fence();
+
+// Entry-point scope for the launch window.
+//  * Elementwise: every device launch of the entry point goes through the
+//    elementwise engine; its kernels may skip the barrier.
+//  * NoStream: the entry point queues no stream work (allocation, queries);
+//    the window is left as it is, so elementwise kernels on either side of
+//    an output allocation can still overlap.  (The allocator's one stream
+//    operation, the synchronisation before it returns cached blocks to HIP,
+//    closes the window itself.)
+//  * Other: closes the window first (stream_fence) and runs with the
+//    overlap off; on the way out it leaves the window empty, so the next
+//    elementwise kernel takes the barrier and so starts after whatever the
+//    entry point queued.
+// Nested entry points never open the window wider than the outer one.
+enum class StreamUse { Other, Elementwise, NoStream };
+class WindowScope {
+public:
+  explicit WindowScope(StreamUse use);
+  ~WindowScope();
+  WindowScope(const WindowScope &) = delete;
+  WindowScope &operator=(const WindowScope &) = delete;
+
+private:
+  StreamUse use_;
+  bool prev_;
+};
+
 // Runs f, converting exceptions into a status code plus a thread-local
-// message.  Every extern "C" entry point is a guard() around its body.
-template <class F> int guard(F &&f) {
+// message.  Every extern "C" entry point is a guard() (or guard_ew()) around
+// its body.
+template <StreamUse USE, class F> int guard_scoped(F &&f) {
   std::lock_guard<std::recursive_mutex> lock(api_mutex());
   try {
     ensure_init();
+    WindowScope scope(USE);
     f();
     return NT_OK;
   } catch (const Error &e) {
@@ -103,6 +146,21 @@ template <class F> int guard(F &&f) {
     set_last_error(e.what());
     return NT_ERR_RUNTIME;
   }
+}
+
+template <class F> int guard(F &&f) {
+  return guard_scoped<StreamUse::Other>(std::forward<F>(f));
+}
+
+// guard() for the entry points whose device work is elementwise-engine
+// kernels only: they may skip the stream barrier (WindowScope).
+template <class F> int guard_ew(F &&f) {
+  return guard_scoped<StreamUse::Elementwise>(std::forward<F>(f));
+}
+
+// guard() for the entry points that queue no stream work.
+template <class F> int guard_nostream(F &&f) {
+  return guard_scoped<StreamUse::NoStream>(std::forward<F>(f));
 }
 
 // guard() for the allocation-free entry points: the library must already be

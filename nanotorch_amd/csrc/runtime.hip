@@ -9,6 +9,8 @@
 #include <map>
 #include <mutex>
 
+#include <hip/hip_ext.h>
+
 #include "caching_allocator.h"
 #include "ew_engine.h"
 
@@ -40,6 +42,12 @@ struct Runtime {
   // kernels may store an nt_status into; read after stream syncs.
   volatile int *deferred_host = nullptr;
   int *deferred_dev = nullptr;
+  // Elementwise kernels queued since the last barrier launch, and whether
+  // the entry point running now may skip the barrier (WindowScope).
+  LaunchWindow window;
+  bool window_open = false;
+  int scope_depth = 0;
+  uint64_t n_unordered = 0, n_ordered = 0, n_fences = 0;
 };
 
 Runtime &rt() {
@@ -60,7 +68,11 @@ struct HipBackend {
     return nullptr;
   }
   static void raw_free(void *p) { NT_HIP_CHECK(hipFree(p)); }
-  static void sync() { NT_HIP_CHECK(hipStreamSynchronize(rt().stream)); }
+  static void sync() {
+    // nt_malloc and nt_free leave the launch window open: close it first.
+    stream_fence();
+    NT_HIP_CHECK(hipStreamSynchronize(rt().stream));
+  }
   [[noreturn]] static void fail_oom(const std::string &msg) {
     fail(NT_ERR_OOM, msg);
   }
@@ -138,6 +150,63 @@ void ensure_init() {
   r.deferred_dev = static_cast<int *>(dword);
   r.available = true;
   r.initialised = true;
+}
+
+// The barrier kernel of stream_fence: no work; its dispatch packet carries
+// the barrier bit, so it starts after every earlier kernel has finished, and
+// work queued after it is ordered after it as usual.
+__global__ void stream_fence_kernel() {}
+
+namespace {
+bool overlap_enabled() {
+  static const bool on = [] {
+    const char *e = std::getenv("NT_OVERLAP");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+} // namespace
+
+uint32_t ew_launch_flags(const ByteRange *reads, int nr,
+                         const ByteRange *writes, int nw) {
+  Runtime &r = rt();
+  const bool allowed = r.window_open && overlap_enabled();
+  if (r.window.admit(reads, nr, writes, nw, allowed)) {
+    ++r.n_unordered;
+    return uint32_t(hipExtAnyOrderLaunch);
+  }
+  ++r.n_ordered;
+  return 0u;
+}
+
+void stream_fence() {
+  Runtime &r = rt();
+  if (r.window.close()) {
+    stream_fence_kernel<<<dim3(1), dim3(64), 0, r.stream>>>();
+    NT_LAUNCH_CHECK();
+    ++r.n_fences;
+  }
+}
+
+WindowScope::WindowScope(StreamUse use) : use_(use), prev_(rt().window_open) {
+  Runtime &r = rt();
+  if (use == StreamUse::Other)
+    stream_fence(); // may throw: nothing else has changed yet
+  r.window_open = use == StreamUse::Elementwise && (r.scope_depth == 0 || prev_);
+  ++r.scope_depth;
+}
+
+WindowScope::~WindowScope() {
+  Runtime &r = rt();
+  --r.scope_depth;
+  r.window_open = prev_;
+  if (use_ == StreamUse::Other) {
+    // The entry point's own launches were all barrier launches (the window
+    // was off), but it may have queued kernels the window does not know
+    // about: the next elementwise kernel must take the barrier.  Nothing in
+    // the window went without it, so no fence is needed.
+    r.window.close();
+  }
 }
 
 bool ew_nontemporal() {
@@ -245,7 +314,7 @@ int nt_sync(void) {
 const char *nt_last_error(void) { return g_last_error.c_str(); }
 
 int nt_malloc(void **ptr, size_t nbytes) {
-  return guard([&] {
+  return guard_nostream([&] {
     if (!ptr)
       fail(NT_ERR_RUNTIME, "nt_malloc: null out pointer");
     *ptr = allocator().alloc(nbytes);
@@ -253,7 +322,7 @@ int nt_malloc(void **ptr, size_t nbytes) {
 }
 
 int nt_free(void *ptr) {
-  return guard([&] {
+  return guard_nostream([&] {
     if (ptr)
       allocator().free(ptr);
   });
@@ -264,7 +333,7 @@ int nt_empty_cache(void) {
 }
 
 int nt_memory_stats(size_t *bytes_in_use, size_t *bytes_cached) {
-  return guard([&] { allocator().stats(bytes_in_use, bytes_cached); });
+  return guard_nostream([&] { allocator().stats(bytes_in_use, bytes_cached); });
 }
 
 int nt_memcpy_h2d(void *dst, const void *src, size_t nbytes) {
@@ -358,7 +427,7 @@ int nt_fill(void *data, int32_t dtype, int64_t n, double value) {
 }
 
 int nt_event_create(void **ev) {
-  return guard([&] {
+  return guard_nostream([&] {
     hipEvent_t e;
     // Timing only: no system-scope release at record time, so a bracket
     // around one launch does not add an L2 write-back to what it measures.
@@ -381,8 +450,20 @@ int nt_event_elapsed_ms(void *start, void *end, float *ms) {
   });
 }
 
+int nt_launch_stats(uint64_t *unordered, uint64_t *ordered, uint64_t *fences) {
+  return guard_nostream([&] {
+    const Runtime &r = rt();
+    if (unordered)
+      *unordered = r.n_unordered;
+    if (ordered)
+      *ordered = r.n_ordered;
+    if (fences)
+      *fences = r.n_fences;
+  });
+}
+
 int nt_event_destroy(void *ev) {
-  return guard([&] {
+  return guard_nostream([&] {
     NT_HIP_CHECK(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
   });
 }
