@@ -239,7 +239,7 @@ def bench_elementwise(steps: int, warmup: int) -> dict:
 # ---------------------------------------------------- config 3: reductions
 
 
-def bench_reductions(iters: int = 8) -> dict:
+def bench_reductions(iters: int = 24) -> dict:
     """Config 3: sum / max / min forward and sum / mean / max backward over
     axis 0, axis 1 and the full [8192, 8192] fp32 tensor, through the C ABI
     with every output preallocated.  Each case runs `iters` launches back to
@@ -922,6 +922,23 @@ PROFILE_CMDS = {
     "mlp_fetch": _PMC.format(c="FETCH_SIZE", d="prof_mlp_fetch", a="--parts mlp --mlp-steps 3 --calib"),
     "mlp_write": _PMC.format(c="WRITE_SIZE", d="prof_mlp_write", a="--parts mlp --mlp-steps 3 --calib"),
 }
+# Transposed-tile variants profiled inside the sweep (the library's
+# NT_TILE_SHAPE / NT_TILE_ORIENT measurement knobs; results are identical):
+# label -> environment prefix.
+TILE_VARIANTS = {
+    "rule": "",
+    "64x64": "NT_TILE_SHAPE=64x64",
+    "64x128": "NT_TILE_SHAPE=64x128",
+    "128x128": "NT_TILE_SHAPE=128x128",
+    "32x256": "NT_TILE_SHAPE=32x256",
+    "keep": "NT_TILE_ORIENT=keep",
+    "swap": "NT_TILE_ORIENT=swap",
+}
+for _lbl, _env in TILE_VARIANTS.items():
+    for _i, _set in ((1, PMC_SET1), (2, PMC_SET2)):
+        PROFILE_CMDS[f"tile_{_lbl}_pmc{_i}"] = ((_env + " ") if _env else "") + _PMC.format(
+            c=_set, d=f"prof_tile_{_lbl}_{_i}", a="--steps 1 --warmup 0 --parts none")
+
 PROFILE_FILES = {
     "sweep": ("elementwise_sweep_config2_trace.md", "Kernel statistics: config-2 elementwise sweep (the headline)"),
     "red": ("reduce_config3_trace.md", "Kernel statistics: config-3 reductions [8192, 8192] fp32"),
@@ -1212,9 +1229,60 @@ def _red_expect(name: str, grid: int) -> str:
     return ""
 
 
+def _summarize_tile_variants(base: str, out_md: str) -> None:
+    """Counter rows of every transposed sweep kernel under each tile variant
+    (TILE_VARIANTS), from the two counter passes per variant under `base`
+    (gpurun_out): which shape and orientation each kernel ran, its duration
+    and what its waves did."""
+    import re
+    cus, simds, clk = 256, 1024, 2.4
+    rows = []
+    for lbl in TILE_VARIANTS:
+        d1, d2 = (os.path.join(base, f"prof_tile_{lbl}_{i}") for i in (1, 2))
+        if not (os.path.isdir(d1) and os.path.isdir(d2)):
+            continue
+        a, b = _load_pmc(d1), _load_pmc(d2)
+        for (name, grid), x in a.items():
+            key = _sweep_key(name)
+            if not key or "|transposed|" not in key:
+                continue
+            y = b.get((name, grid), {})
+            m = re.search(r"true, (\d+), (\d+),", name)
+            cyc = x["dur_ns"] * clk
+            wc = max(x.get("SQ_WAVE_CYCLES", 0.0), 1.0)
+            rows.append((key, lbl, f"{m.group(1)}x{m.group(2)}" if m else "?", x["dur_ns"] / 1e3,
+                         wc * 4 / (cus * cyc), x.get("SQ_WAIT_ANY", 0.0) / wc,
+                         x.get("SQ_WAIT_INST_ANY", 0.0) / wc,
+                         y.get("SQ_ACTIVE_INST_VALU", 0.0) * 4 / (simds * cyc) if y else float("nan"),
+                         x.get("SQ_LDS_BANK_CONFLICT", 0.0) / (cus * cyc)))
+    nb = {k: ew_bytes(k.split("|")[0], k.split("|")[2]) for k, *_ in rows}
+    with open(out_md, "w") as o:
+        o.write("# Transposed elementwise kernels under each tile variant (config-2 sweep)\n\n"
+                "Commands (repo root on the GPU box), two counter passes per variant:\n\n```\n")
+        for lbl in TILE_VARIANTS:
+            o.write(PROFILE_CMDS[f"tile_{lbl}_pmc1"] + "\n" + PROFILE_CMDS[f"tile_{lbl}_pmc2"] + "\n")
+        o.write("```\n\nSummarised with `python bench.py --summarize tile_variants gpurun_out`.  "
+                "`rule` is the library's choice; the other variants force one compiled fp32 tile "
+                "shape (the orientation still by the cost rule) or one orientation (the shape still "
+                "by the rule) for every transposed kernel of the sweep (NT_TILE_SHAPE / "
+                "NT_TILE_ORIENT; results are identical).  Durations are from the counter-collecting "
+                "pass (kernels serialised); frac = algorithmic bytes / duration / 8 TB/s.  Columns as "
+                "in elementwise_sweep_config2_counters.md: waves/CU resident, wait = s_waitcnt / "
+                "barrier share of wave time, issue-wait = ready but not issued, VALU busy = SIMD "
+                "cycles issuing VALU, bank-conflict = LDS bank-conflict cycles per CU / cycles.\n\n"
+                "| kernel | variant | tile | us | frac | waves/CU | wait | issue-wait | VALU busy | "
+                "bank-conflict |\n|---|---|---|---|---|---|---|---|---|---|\n")
+        for key, lbl, tile, us, wv, w, iw, vb, bc in sorted(rows, key=lambda r: (r[0], r[3])):
+            o.write(f"| {key} | {lbl} | {tile} | {us:.1f} | {nb[key] / (us * 1e-6) / 8e12:.3f} | "
+                    f"{wv:.1f} | {w:.2f} | {iw:.2f} | {vb:.2f} | {bc:.3f} |\n")
+
+
 def summarize(kind: str, dirs: list[str]) -> None:
     import csv
     prof = os.path.join(ROOT, "profiles")
+    if kind == "tile_variants":
+        _summarize_tile_variants(dirs[0], os.path.join(prof, "elementwise_transposed_tile_variants.md"))
+        return
     if kind == "ew_pmc":
         _summarize_pmc("ew", dirs, os.path.join(prof, "elementwise_sweep_config2_counters.md"),
                        "Issue and wait counters: config-2 elementwise sweep kernels",

@@ -1018,7 +1018,8 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       else if (sr == 1 && sc != 0) // column-major now
         cost_keep += wgt;
     }
-    if (cost_swap < cost_keep) {
+    const TileOverride &ov = tile_override();
+    if (ov.orient == 2 || (ov.orient == 0 && cost_swap < cost_keep)) {
       std::swap(R0, C0);
       for (int k = 0; k < NT; ++k)
         std::swap(st[k][0], st[k][1]);
@@ -1106,6 +1107,14 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       if constexpr (std::is_same_v<TI, float> && std::is_same_v<TO, float>) {
         const int n_col = __builtin_popcount(col_in) + __builtin_popcount(col_out);
         const int n_row = __builtin_popcount(row_in) + __builtin_popcount(row_out);
+        if (ov.tr == 64 && ov.tc == 64)
+          return tile4.template operator()<64, 64>();
+        if (ov.tr == 64 && ov.tc == 128)
+          return tile4.template operator()<64, 128>();
+        if (ov.tr == 128 && ov.tc == 128)
+          return tile4.template operator()<128, 128>();
+        if (ov.tr == 32 && ov.tc == 256)
+          return tile4.template operator()<32, 256>();
         if (n_col == 1 && n_row >= 3)
           return tile4.template operator()<32, 256>();
         if (n_col == 1 && !ew_heavy<F>())

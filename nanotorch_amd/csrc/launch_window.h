@@ -16,7 +16,7 @@
 // when
 //   * it writes nothing that a window kernel reads or writes, and reads
 //     nothing that a window kernel writes;
-//   * the window holds at least one and fewer than MAX_KERNELS kernels.
+//   * the window holds at least one and fewer than limit() kernels.
 // Otherwise the kernel is launched with the barrier and starts a new window.
 //
 // Host-only code (no HIP header), so a CPU test exercises it directly.
@@ -36,11 +36,16 @@ struct ByteRange {
 
 class LaunchWindow {
 public:
-  // Barrier launches every MAX_KERNELS kernels at most: in a sweep of
-  // independent 2^24-element kernels on one MI355X, a barrier every 6th
-  // launch was fastest (every 2nd, 3rd, 4th, 12th: within 2%).
-  static constexpr int MAX_KERNELS = 6;
+  // At most MAX_KERNELS kernels per window (a barrier launch at least every
+  // limit() kernels); the limit is set at run time up to that.
+  static constexpr int MAX_KERNELS = 16;
+  static constexpr int DEFAULT_LIMIT = 12;
   static constexpr int MAX_RANGES = 16; // operands per kernel
+
+  void set_limit(int k) {
+    limit_ = k < 1 ? 1 : (k > MAX_KERNELS ? MAX_KERNELS : k);
+  }
+  int limit() const { return limit_; }
 
   // Records a kernel reading `reads` and writing `writes`; true when it may
   // be launched without the barrier.  More than MAX_RANGES ranges of either
@@ -48,7 +53,7 @@ public:
   bool admit(const ByteRange *reads, int nr, const ByteRange *writes, int nw,
              bool allowed) {
     const bool fits = nr <= MAX_RANGES && nw <= MAX_RANGES;
-    bool free_of_hazards = allowed && fits && n_ > 0 && n_ < MAX_KERNELS;
+    bool free_of_hazards = allowed && fits && n_ > 0 && n_ < limit_;
     for (int k = 0; k < n_ && free_of_hazards; ++k) {
       const Entry &e = win_[k];
       for (int i = 0; i < nw && free_of_hazards; ++i) {
@@ -102,6 +107,7 @@ private:
     ByteRange r[MAX_RANGES], w[MAX_RANGES];
   };
   Entry win_[MAX_KERNELS];
+  int limit_ = DEFAULT_LIMIT;
   int n_ = 0;
   bool unordered_ = false;
 };

@@ -100,6 +100,18 @@ uint32_t ew_launch_flags(const ByteRange *reads, int nr,
 // kernel has finished.
 void stream_fence();
 
+// Measurement knobs of the transposed-tile kernels (fp32), read once from
+// the environment: NT_TILE_SHAPE=<rows>x<cols> forces one of the compiled
+// shapes (64x64, 64x128, 128x128, 32x256; 0 = the shape rule), and
+// NT_TILE_ORIENT=keep|swap forces the orientation (0 = the cost rule).
+// Results do not depend on them; they exist so that each shape can be
+// profiled inside the full sweep.
+struct TileOverride {
+  int tr = 0, tc = 0;
+  int orient = 0; // 0 rule, 1 keep, 2 swap
+};
+const TileOverride &tile_override();
+
 // Entry-point scope for the launch window.
 //  * Elementwise: every device launch of the entry point goes through the
 //    elementwise engine; its kernels may skip the barrier.

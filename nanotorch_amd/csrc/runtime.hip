@@ -5,7 +5,9 @@
 // checks), src/cpp/allocator.{h,cpp} (caching allocator), src/cpp/storage.cpp
 // (allocate/to/clone) and src/cpp/factory.cu (fills).
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 
@@ -148,6 +150,9 @@ void ensure_init() {
   NT_HIP_CHECK(hipHostGetDevicePointer(&dword, word, 0));
   r.deferred_host = static_cast<volatile int *>(word);
   r.deferred_dev = static_cast<int *>(dword);
+  // Kernels per launch window (launch_window.h); NT_OVERLAP_WINDOW overrides.
+  if (const char *w = std::getenv("NT_OVERLAP_WINDOW"))
+    r.window.set_limit(std::atoi(w));
   r.available = true;
   r.initialised = true;
 }
@@ -207,6 +212,25 @@ WindowScope::~WindowScope() {
     // the window went without it, so no fence is needed.
     r.window.close();
   }
+}
+
+const TileOverride &tile_override() {
+  static const TileOverride o = [] {
+    TileOverride t;
+    if (const char *e = std::getenv("NT_TILE_SHAPE")) {
+      int a = 0, b = 0;
+      if (std::sscanf(e, "%dx%d", &a, &b) == 2 &&
+          ((a == 64 && (b == 64 || b == 128)) || (a == 128 && b == 128) ||
+           (a == 32 && b == 256))) {
+        t.tr = a;
+        t.tc = b;
+      }
+    }
+    if (const char *e = std::getenv("NT_TILE_ORIENT"))
+      t.orient = std::strcmp(e, "keep") == 0 ? 1 : (std::strcmp(e, "swap") == 0 ? 2 : 0);
+    return t;
+  }();
+  return o;
 }
 
 bool ew_nontemporal() {

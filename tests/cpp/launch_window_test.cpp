@@ -60,6 +60,7 @@ int main() {
     std::mt19937_64 g(1000 + trial);
     const uintptr_t space = (trial % 4 == 0) ? 64 : ((trial % 4 == 1) ? 4096 : (1u << 20));
     LaunchWindow win;
+    win.set_limit(1 + trial % LaunchWindow::MAX_KERNELS);
     std::vector<K> ks;
     int last_barrier = -1;
     for (int step = 0; step < 500; ++step) {
@@ -94,7 +95,7 @@ int main() {
       ++launched;
       if (free_) {
         ++admitted;
-        if (!allowed || before == 0 || before >= LaunchWindow::MAX_KERNELS) {
+        if (!allowed || before == 0 || before >= win.limit()) {
           std::printf("admitted against the rules (trial %d step %d)\n", trial, step);
           ++errors;
         }
@@ -112,7 +113,7 @@ int main() {
       // a barrier asked for with room in the window, permission and no
       // hazard against the window would be a missed overlap (not unsafe,
       // but the window must do what it says)
-      if (k.barrier && allowed && before > 0 && before < LaunchWindow::MAX_KERNELS) {
+      if (k.barrier && allowed && before > 0 && before < win.limit()) {
         bool any = false;
         for (int i = j - before; i < j; ++i)
           any = any || hazard(ks[i], k);
