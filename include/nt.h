@@ -284,6 +284,16 @@ int nt_reduce_bwd(int32_t op, const nt_view *g, double scale, const nt_view *idx
 int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
               int32_t accumulate);
 
+/* No single counterpart in the reference: its Linear layer computes
+ * `x @ W + b` as MatmulOp then AddOp, two kernels (src/nanotorch/nn/
+ * module.py:73-75 over matmul.cu:207-279 and binary_ops.cu:178).  This is
+ * that pair in one call: c[..., i, j] = fl(sum_k a[..., i, k] b[..., k, j])
+ * + bias[j], the bias added in the product's epilogue with the same two
+ * fp32 roundings (the product's, then the add's).  float32 only
+ * (NT_ERR_VALUE otherwise); bias is 1-D with one value per column of c. */
+int nt_matmul_bias(const nt_view *a, const nt_view *b, const nt_view *bias,
+                   const nt_view *c);
+
 /* --------------------------------------------------------------- indexing */
 
 /* Replaces `gather_from_axes` (src/cpp/ops/copy_ops.cu:93-160, host only in

@@ -297,6 +297,19 @@ def matmul(x1, x2, out_shape) -> Storage:
     return out
 
 
+def matmul_bias(x1, x2, bias, out_shape) -> Storage:
+    """x1 @ x2 + bias (2-D float32 views, bias 1-D over the columns) in one
+    product whose epilogue adds the bias: the same two fp32 roundings as the
+    product followed by a broadcast add."""
+    require_device(x1, x2, bias)
+    out = Storage.allocate(_numel(out_shape), x1.dtype, Device.Cuda)
+    v1, v2, vb = view_of(x1), view_of(x2), view_of(bias)
+    vo = flat_view(out, out_shape)
+    _lib.call("nt_matmul_bias", ctypes.byref(v1), ctypes.byref(v2), ctypes.byref(vb),
+              ctypes.byref(vo))
+    return out
+
+
 def matmul_into(x1, x2, target, accumulate: bool) -> None:
     require_device(x1, x2, target)
     v1, v2, vo = view_of(x1), view_of(x2), view_of(target)

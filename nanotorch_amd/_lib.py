@@ -81,6 +81,7 @@ _SIGNATURES = {
         [c_int32, _VP, c_double, _VP, _VP, POINTER(c_int64), c_int32, _VP, c_int32],
     ),
     "nt_matmul": (c_int, [_VP, _VP, _VP, c_int32]),
+    "nt_matmul_bias": (c_int, [_VP, _VP, _VP, _VP]),
     "nt_gather_axes": (
         c_int,
         [_VP, _VP, c_int32, POINTER(c_int32), _VP, POINTER(c_int32), POINTER(c_int32)],

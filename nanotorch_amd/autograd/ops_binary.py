@@ -244,6 +244,61 @@ class MatmulOp(Function):
         return B * (M * Kd + Kd * N + M * N) * sizeof(promote_dtypes(x1.dtype, x2.dtype))
 
 
+class LinearOp(Function):
+    """x @ W + b for 2-D float32 device operands in one product whose
+    epilogue adds b (nt_matmul_bias): the reference's Linear forward, a
+    MatmulOp then an AddOp (src/nanotorch/nn/module.py:73-75), with the same
+    two fp32 roundings (the product's, then the add's).  Its backward is
+    those two ops' backward: dx = g . W^T and dW = x^T . g (MatmulOp,
+    ops_binary.py:253-267, each one product reading the transposed operand
+    in place), db = g summed over the rows (AddOp's unbroadcast, :49-50)."""
+
+    def forward(self, x: Tensor, W: Tensor, b: Tensor) -> Tensor:
+        self.save_for_backward(x, W)
+        self._b_shape = b.shape
+        shape = (x.shape[0], W.shape[1])
+        return Tensor._new_contiguous(K.matmul_bias(x, W, b, shape), shape)
+
+    def backward(self, grad_out: Tensor) -> tuple[Tensor, ...]:
+        x, W = self.saved_tensors
+        return (grad_out @ W.transpose(0, 1), x.transpose(0, 1) @ grad_out,
+                unbroadcast(grad_out, self._b_shape))
+
+    def fused_ok(self) -> bool:
+        return True
+
+    def _backward_into(self, g: Tensor, needs, targets):
+        x, W = self.saved_tensors
+        results = [None, None, None]
+        for i, (lhs, rhs, shape) in enumerate(((g, W.transpose(0, 1), x.shape),
+                                               (x.transpose(0, 1), g, W.shape))):
+            if not needs[i]:
+                continue
+            if targets[i] is None:
+                results[i] = Tensor._new_contiguous(K.matmul(lhs, rhs, shape), shape)
+            else:
+                K.matmul_into(lhs, rhs, targets[i], accumulate=True)
+                results[i] = targets[i]
+        if needs[2]:
+            r = unbroadcast(g, self._b_shape)
+            if targets[2] is None:
+                results[2] = r
+            else:
+                K.inplace(_lib.ADD, targets[2], r)
+                results[2] = targets[2]
+        return results
+
+    @classmethod
+    def usable(cls, x: Tensor, W: Tensor, b: Tensor) -> bool:
+        """Whether the fused form applies: 2-D float32 x and W and a 1-D
+        float32 b over W's columns, all on the device."""
+        from .._data_type import Dtype
+        from ..cuda import Device
+        return (x.ndim == 2 and W.ndim == 2 and b.ndim == 1 and b.shape[0] == W.shape[1]
+                and x.shape[1] == W.shape[0]
+                and all(t.device == Device.Cuda and t.dtype == Dtype.Float32 for t in (x, W, b)))
+
+
 def _binary_kernel_op(x1: Tensor, x2: Tensor, op: int, out: Tensor | None = None) -> Tensor:
     """Promotion + broadcast + kernel call, with the reference's ``out=``
     semantics (ops_binary.py:283-315): ``out is x1`` runs in place, any other

@@ -147,21 +147,27 @@ enum : int { ST_PLAIN = 0, ST_STREAM = 1, ST_THROUGH = 2 };
 // Which one-output kernels store through, by kernel kind.  Kernels queued
 // back to back share the cost of the streaming stores' dirty L2 lines: a
 // kernel that leaves them makes the next one slower while they drain, so
-// per-kernel times move between neighbours and the totals decide.  With the
+// per-kernel times move between neighbours and the totals decide.  Measured
+// on one MI355X, alternating builds on the same box, with the sweep queuing
+// each layout's forwards before its backwards and independent kernels
+// overlapping: every flat and tile kernel streaming its stores, against the
 // flat kernels, the transposed tiles and the max/min backward over all axes
-// storing through, against every store streaming (one MI355X, two rounds per
-// build): config-2 sweep 5780-5788 -> 5848-5857 GB/s (+1.2%; per kernel the
-// accumulating backwards gain 8-13% and the transposed forwards lose 2-6%,
-// as each kernel now pays for its own writes), config-3 reductions
-// 6374-6387 -> 6466-6476 GB/s (+1.4%; the sum / mean / max backwards over
-// all axes +4-18%), config-5 step unchanged within its run-to-run spread.
-// The rows kernel (sum / mean backward along one axis, bias adds) and the
-// 2-D max/min backward storing through as well cost the reductions 1%
-// (axis-1 backwards -3 to -14%, axis 0 +7%): they keep streaming stores.
+// storing through, config-2 sweep 5929-5939 -> 5989-6006 GB/s (+1.1%; the
+// dominant kernel 0.683-0.686 -> 0.703-0.708), config-3 and config-5 within
+// 1% except one kernel: a flat kernel whose inputs are all broadcast scalars
+// (a pure write, the mean backward over all axes) fell from 0.874 to 0.779
+// of peak streaming.  So the flat kernel stores through at run time exactly
+// when it reads no full operand (ew_flat_kernel's `through`), the max/min
+// backward over all axes (TK_SELVEC) always, everything else streams.  (In
+// an earlier sweep that queued each backward right after its forward,
+// storing through measured 1.2% faster: the backwards then re-read outputs
+// the forwards had just written.)  NT_THROUGH_KINDS overrides the
+// compile-time set.
 enum : int { TK_FLAT = 1, TK_ROWS = 2, TK_TILE = 4, TK_SEL2D = 8, TK_SELVEC = 16 };
-constexpr bool through_pays(int kind) {
-  return kind == TK_FLAT || kind == TK_TILE || kind == TK_SELVEC;
-}
+#ifndef NT_THROUGH_KINDS
+#define NT_THROUGH_KINDS (TK_SELVEC)
+#endif
+constexpr bool through_pays(int kind) { return (kind & (NT_THROUGH_KINDS)) != 0; }
 
 // The form a kernel of kind KIND with NOUT output streams uses when
 // streaming is on.
@@ -270,7 +276,7 @@ template <class TI, class TO, int NI, int NO, int VEC, int UNROLL, bool NTL,
           class F>
 __global__ __launch_bounds__(FLAT_THREADS) void ew_flat_kernel(
     PtrPack<const TI, NI> in, uint32_t scalar_mask, PtrPack<TO, NO> out,
-    int64_t nvec, int64_t n, F f) {
+    int64_t nvec, int64_t n, bool through, F f) {
   using VI = VecT<TI, VEC>;
   using VO = VecT<TO, VEC>;
   // wg0: the workgroup's first vector (its outputs start there: a uniform
@@ -313,9 +319,16 @@ __global__ __launch_bounds__(FLAT_THREADS) void ew_flat_kernel(
           o[m].v[j] = y[m];
       }
 #pragma unroll
-      for (int m = 0; m < NO; ++m)
+      for (int m = 0; m < NO; ++m) {
+        if constexpr (NTL && NO == 1) {
+          if (through) { // a pure write (every input a broadcast scalar)
+            vstore_through<TO, VEC>(out.p[m] + wg0 * VEC, (vi - wg0) * VEC, o[m]);
+            continue;
+          }
+        }
         vstore_out<NTL, NO, TK_FLAT, TO, VEC>(out.p[m] + wg0 * VEC, (vi - wg0) * VEC,
-                                     true, o[m]);
+                                              true, o[m]);
+      }
     }
   }
   // Fewer than VEC trailing elements: block 0 takes them one per thread.
@@ -915,15 +928,20 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       const int64_t blocks = std::max<int64_t>(
           1, (cv + FLAT_THREADS * UNROLL - 1) / (FLAT_THREADS * UNROLL));
       const dim3 grid{unsigned(blocks), 1u, 1u};
+      // a workgroup's outputs lie within FLAT_THREADS * UNROLL vectors of
+      // its base: within the device-scope stores' 2^31-byte range
+      const bool through =
+          smask == (NI > 0 ? (1u << NI) - 1 : 0u) &&
+          int64_t(FLAT_THREADS) * UNROLL * VBIG * int64_t(sizeof(TO)) <= BUF_BYTES;
       if (aligned && ntl)
         ew_launch(ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, true, F>, grid,
-                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, f);
+                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, through, f);
       else if (aligned)
         ew_launch(ew_flat_kernel<TI, TO, NI, NO, VBIG, UNROLL, false, F>, grid,
-                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, f);
+                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, false, f);
       else
         ew_launch(ew_flat_kernel<TI, TO, NI, NO, 1, UNROLL, false, F>, grid,
-                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, f);
+                  FLAT_THREADS, s, flags, cin, smask, cout, cv, cn, false, f);
       NT_LAUNCH_CHECK();
       v0 += cv;
     } while (v0 < nvec);

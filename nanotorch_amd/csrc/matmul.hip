@@ -82,6 +82,11 @@ struct MMArgs {
   // split (kslice == K), results go to C.
   int64_t kslice;
   float *part;
+  // Optional bias added to every output row in the epilogue, C = fl(acc) +
+  // bias[n] (one fp32 rounding after the product's own, as a separate add
+  // would give); nullptr: none.  Never combined with accumulate.
+  const float *bias;
+  int64_t sBias;
 };
 
 // Operand tile loader: global -> registers -> LDS.  ROWS x MM_BK tile of
@@ -222,7 +227,7 @@ __device__ __forceinline__ void mm_epilogue(const MMArgs &g, const TileCoord &tc
         if (row < g.M) {
           float *dst = tc.C + row * g.sCm + col * g.sCn;
           const float v = acc[i][j][r];
-          *dst = g.accumulate ? (*dst + v) : v;
+          *dst = g.accumulate ? (*dst + v) : (g.bias ? v + g.bias[col * g.sBias] : v);
         }
       }
     }
@@ -629,7 +634,7 @@ __global__ __launch_bounds__(WD_THREADS, 1) void mm_f32_mfma_wide_kernel(
           g.part[(int64_t(blockIdx.y) * g.M + row) * g.N + col] = v;
         } else {
           float *dst = tc.C + row * g.sCm + col * g.sCn;
-          *dst = g.accumulate ? (*dst + v) : v;
+          *dst = g.accumulate ? (*dst + v) : (g.bias ? v + g.bias[col * g.sBias] : v);
         }
       }
     }
@@ -641,7 +646,8 @@ __global__ __launch_bounds__(WD_THREADS, 1) void mm_f32_mfma_wide_kernel(
 template <int S, bool VEC_C>
 __global__ __launch_bounds__(256) void mm_splitk_sum_kernel(
     const float *__restrict__ part, int64_t M, int64_t N, float *C,
-    int64_t sCm, int64_t sCn, int accumulate, FastDivU32 fdn4, uint32_t total) {
+    int64_t sCm, int64_t sCn, int accumulate, const float *__restrict__ bias,
+    int64_t sBias, FastDivU32 fdn4, uint32_t total) {
   // one work-item per 4 columns of one row, in a one-shot grid; the S slice
   // loads are independent (S is a template argument) and go out together
   const uint32_t q = blockIdx.x * 256u + threadIdx.x;
@@ -663,6 +669,12 @@ __global__ __launch_bounds__(256) void mm_splitk_sum_kernel(
     v.y = v.y + w[s].y;
     v.z = v.z + w[s].z;
     v.w = v.w + w[s].w;
+  }
+  if (bias) { // the product's value, then the bias add (its own rounding)
+    v.x = v.x + bias[(n + 0) * sBias];
+    v.y = v.y + bias[(n + 1) * sBias];
+    v.z = v.z + bias[(n + 2) * sBias];
+    v.w = v.w + bias[(n + 3) * sBias];
   }
   if constexpr (VEC_C) {
     float4 *dst = reinterpret_cast<float4 *>(C + m * sCm + n);
@@ -779,12 +791,12 @@ template <int LA, int LB> void launch_mfma(const MMArgs &a, int64_t blocks) {
   do {                                                                         \
     if (vec_c)                                                                 \
       mm_splitk_sum_kernel<SS, true><<<grid, 256, 0, stream()>>>(              \
-          w.part, a.M, a.N, a.C, a.sCm, a.sCn, a.accumulate, fdn4,             \
-          uint32_t(items));                                                    \
+          w.part, a.M, a.N, a.C, a.sCm, a.sCn, a.accumulate, a.bias, a.sBias,  \
+          fdn4, uint32_t(items));                                              \
     else                                                                       \
       mm_splitk_sum_kernel<SS, false><<<grid, 256, 0, stream()>>>(             \
-          w.part, a.M, a.N, a.C, a.sCm, a.sCn, a.accumulate, fdn4,             \
-          uint32_t(items));                                                    \
+          w.part, a.M, a.N, a.C, a.sCm, a.sCn, a.accumulate, a.bias, a.sBias,  \
+          fdn4, uint32_t(items));                                              \
   } while (0)
           if (S == 2)
             NT_SPLITK_SUM(2);
@@ -827,11 +839,13 @@ bool aligned16(const void *p) {
 
 using namespace nt;
 
-extern "C" {
+namespace {
 
-int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
-              int32_t accumulate) {
-  return guard([&] {
+// C (+)= A . B, or C = A . B + bias (bias: one value per column of C,
+// fp32 only, never with accumulate).
+void matmul_run(const nt_view *a, const nt_view *b, const nt_view *c,
+                int32_t accumulate, const nt_view *bias) {
+  {
     check_view(a, "matmul");
     check_view(b, "matmul");
     check_view(c, "matmul");
@@ -856,8 +870,36 @@ int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
     int64_t nbatch = 1;
     for (int d = 0; d < nb; ++d)
       nbatch *= a->shape[d];
+    if (bias) {
+      check_view(bias, "matmul_bias");
+      if (a->dtype != NT_FLOAT32 || bias->dtype != NT_FLOAT32)
+        fail(NT_ERR_VALUE, "matmul_bias: float32 operands only");
+      if (accumulate)
+        fail(NT_ERR_RUNTIME, "matmul_bias: no accumulate form");
+      if (bias->ndim != 1 || bias->shape[0] != N)
+        fail(NT_ERR_RUNTIME, "matmul_bias: bias must be 1-D with one value per column");
+    }
     if (M == 0 || N == 0 || nbatch == 0)
       return;
+    if (K == 0 && bias) {
+      // C = fl(0 + bias), the bias broadcast over the rows (and batches), as
+      // the empty product followed by the add gives (a -0.0 bias gives +0.0)
+      DeviceScratch zero_buf(sizeof(float));
+      if (nt_fill(zero_buf.get(), NT_FLOAT32, 1, 0.0) != NT_OK)
+        fail(NT_ERR_RUNTIME, nt_last_error());
+      nt_view zv = *c, bv = *c;
+      zv.data = zero_buf.get();
+      zv.offset = 0;
+      bv.data = bias->data;
+      bv.offset = bias->offset;
+      for (int d = 0; d < nd; ++d)
+        zv.strides[d] = bv.strides[d] = 0;
+      bv.strides[nd - 1] = bias->strides[0];
+      const int rc = nt_binary(NT_ADD, &zv, &bv, c);
+      if (rc != NT_OK)
+        fail(rc, nt_last_error());
+      return;
+    }
     if (K == 0) {
       if (!accumulate) {
         dispatch_arith(c->dtype, [&]<class T>() {
@@ -913,6 +955,8 @@ int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
       g.accumulate = accumulate ? 1 : 0;
       g.kslice = K;
       g.part = nullptr;
+      g.bias = bias ? typed_ptr<const float>(bias) : nullptr;
+      g.sBias = bias ? bias->strides[0] : 0;
       // Vector (16-byte) tile loads need the unit-stride extent and the other
       // stride to be multiples of 4 and a 16-byte aligned base.
       int la = LAY_GEN, lb = LAY_GEN;
@@ -976,7 +1020,21 @@ int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
       mm_simt_kernel<T><<<grid, 256, 0, stream()>>>(g);
       NT_LAUNCH_CHECK();
     });
-  });
+  }
+}
+
+} // namespace
+
+extern "C" {
+
+int nt_matmul(const nt_view *a, const nt_view *b, const nt_view *c,
+              int32_t accumulate) {
+  return guard([&] { matmul_run(a, b, c, accumulate, nullptr); });
+}
+
+int nt_matmul_bias(const nt_view *a, const nt_view *b, const nt_view *bias,
+                   const nt_view *c) {
+  return guard([&] { matmul_run(a, b, c, 0, bias); });
 }
 
 } // extern "C"

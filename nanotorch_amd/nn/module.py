@@ -4,7 +4,9 @@
 ``z = sqrt(6 / fan_in)`` and zero bias; the arithmetic runs in float32 on the
 device (same three roundings as the reference's host loop), so parameters
 start on ``device`` (default "cuda").  ``Sigmoid`` is added next to ReLU and
-Tanh (the reference exposes sigmoid only as a function).
+Tanh (the reference exposes sigmoid only as a function).  ``Linear.forward``
+on float32 device tensors runs the product and the bias add as one kernel
+(``LinearOp``): same values and gradients as the reference's two ops.
 """
 
 from __future__ import annotations
@@ -13,6 +15,7 @@ import math
 from typing import Any, Sequence
 
 from ..autograd import ReluOp, SigmoidOp, TanhOp
+from ..autograd.ops_binary import LinearOp
 from ..core import Tensor
 from ..cuda import Device
 from ..factories import rand, zeros
@@ -55,6 +58,9 @@ class Linear(Module):
             raise NotImplementedError(f"Can only forward a 2D tensor for now, got {x.ndim}")
         if x.shape[1] != self._W.shape[0]:
             raise ValueError(f"Cannot align axes of size {x.shape[1]} and {self._W.shape[0]}.")
+        if self._b is not None and LinearOp.usable(x, self._W, self._b):
+            # the product and the bias add in one kernel, same roundings
+            return LinearOp.apply(x, self._W, self._b)
         z = x @ self._W
         if self._b is not None:
             z = z + self._b

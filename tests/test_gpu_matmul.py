@@ -178,3 +178,71 @@ def test_wide_tile_split_k_full_check(gpu, accumulate, layout):
     scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64) + (
         np.abs(old) if accumulate else 0.0)
     assert_rel(host(tgt), want, 1e-4, f"split-K accumulate={accumulate}", scale=scale)
+
+
+# ----------------------------------------------------- bias in the epilogue
+
+BIAS_SHAPES = [(7, 5, 3), (129, 33, 130), (300, 257, 512),  # generic / edge tiles
+               (1024, 512, 768),                            # 128x128 MFMA kernels
+               (4096, 1024, 4096),                          # wide kernel, one pass
+               (1024, 8192, 256),                           # wide kernel, split K
+               (64, 0, 96)]                                  # K = 0: C = bias
+
+
+@pytest.mark.parametrize("layout", ["NN", "TN"])
+@pytest.mark.parametrize("M,K_,N", BIAS_SHAPES)
+def test_matmul_bias_equals_product_then_add(gpu, M, K_, N, layout):
+    """nt_matmul_bias (the bias added in the product's epilogue) against the
+    same product from nt_matmul followed by the broadcast add kernel, bit for
+    bit: the fused form keeps the two fp32 roundings of the reference's
+    MatmulOp then AddOp."""
+    r = rng(seed_of("mmbias", M, K_, N, layout))
+    a = r.standard_normal((M, K_)).astype(np.float32)
+    b = (r.standard_normal((K_, N)) / np.sqrt(max(K_, 1))).astype(np.float32)
+    bias = r.standard_normal(N).astype(np.float32)
+    ta = dev(a) if layout == "NN" else dev_T(a)
+    tb, tbias = dev(b), dev(bias)
+    fused = host(nt.Tensor._new_contiguous(K.matmul_bias(ta, tb, tbias, (M, N)), (M, N)))
+    prod = nt.Tensor._new_contiguous(K.matmul(ta, tb, (M, N)), (M, N))
+    want = host(prod + tbias)
+    assert_bitexact(fused, want, f"bias {M}x{K_}x{N} {layout}")
+
+
+def test_matmul_bias_rejects_bad_operands(gpu):
+    a, b = dev(np.ones((4, 3), np.float32)), dev(np.ones((3, 5), np.float32))
+    with pytest.raises(RuntimeError):
+        K.matmul_bias(a, b, dev(np.ones(4, np.float32)), (4, 5))  # wrong length
+    with pytest.raises(ValueError):
+        K.matmul_bias(dev(np.ones((4, 3))), dev(np.ones((3, 5))), dev(np.ones(5)), (4, 5))
+
+
+def test_linear_fused_forward_and_backward_match_the_composition(gpu):
+    """nn.Linear on float32 device tensors (LinearOp: product + bias in one
+    kernel) against the reference's composition x @ W + b through the
+    Tensor API, bit for bit: output, dx, dW, db, first-write and
+    accumulated."""
+    from nanotorch_amd import nn
+    r = rng(seed_of("linear-fused"))
+    x = r.standard_normal((512, 256)).astype(np.float32)
+    g = r.standard_normal((512, 384)).astype(np.float32)
+    lin = nn.Linear(256, 384)
+    W0 = host(lin._W)
+    lin._b = dev(r.standard_normal(384).astype(np.float32), requires_grad=True)
+    b0 = host(lin._b)
+    results = []
+    for fused in (True, False):
+        W = dev(W0, requires_grad=True)
+        b = dev(b0, requires_grad=True)
+        X = dev(x, requires_grad=True)
+        G = dev(g)
+        for _ in range(2):  # the second pass accumulates into the grads
+            if fused:
+                lin._W, lin._b = W, b
+                z = lin(X)
+                assert type(z.grad_fn).__name__ == "LinearOp"
+            else:
+                z = X @ W + b
+            (z * G).sum().backward()
+        results.append([host(z), host(X.grad), host(W.grad), host(b.grad)])
+    for name, f, c in zip(("z", "dx", "dW", "db"), *results):
+        assert_bitexact(f, c, name)
