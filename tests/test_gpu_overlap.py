@@ -185,3 +185,65 @@ def test_reused_allocations_wait_for_their_readers(gpu):
         assert_bitexact(host(y), prev * np.float32(2.0), f"step {i}")
     assert_bitexact(host(cur_t), cur, "final")
     assert reused >= 6, reused  # the hazard this test is about did occur
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_op_streams_match_host(gpu, seed):
+    """A random stream of elementwise ops over a pool of six 2^22-element
+    tensors (each op reads one or two pool tensors, possibly its own
+    destination, possibly through a `.T` view, and writes one), with a
+    reduction or a device-to-host copy every few ops: every read-after-
+    write, write-after-read and write-after-write between nearby ops is
+    a hazard the launch window must order.  The same stream runs on the
+    host in float32 (add, sub, neg, exact scalings and copies: every
+    result exact), and every tensor must match bit for bit at each
+    check and at the end."""
+    r = rng(seed_of("overlap-random", seed))
+    side = 2048
+    pool_h = [r.integers(-8, 9, (side, side)).astype(np.float32) for _ in range(6)]
+    pool_d = [dev(a) for a in pool_h]
+    half, two = np.float32(0.5), np.float32(2.0)
+    pool_d[0] * 0.5
+    pool_d[0] * 2.0  # the device scalars, built and cached first
+    nt.sync()
+    s0 = _stats()
+    for step in range(160):
+        kind = int(r.integers(0, 10))
+        dst, a, b = (int(v) for v in r.integers(0, 6, 3))
+        tr_a = bool(r.integers(0, 4) == 0)  # read a through a .T view
+        A_h = pool_h[a].T if tr_a else pool_h[a]
+        A_d = pool_d[a].T if tr_a else pool_d[a]
+        if kind == 9 and step % 3 == 0:
+            # other stream work: a device-to-host copy or a reduction
+            if r.integers(0, 2):
+                assert_bitexact(host(pool_d[a]), pool_h[a], f"copy at step {step}")
+            else:
+                got = float(host(pool_d[a].sum()))
+                want = float(np.sum(pool_h[a].astype(np.float64)))
+                assert abs(got - want) <= 1e-5 * float(np.sum(np.abs(pool_h[a]))) + 1e-30
+            continue
+        if kind < 3:
+            res_h = A_h + pool_h[b]
+            K.copy_view(A_d + pool_d[b], pool_d[dst])
+        elif kind < 5:
+            res_h = A_h - pool_h[b]
+            K.copy_view(A_d - pool_d[b], pool_d[dst])
+        elif kind < 6:
+            res_h = -A_h
+            K.copy_view(-A_d, pool_d[dst])
+        elif kind < 8:
+            big = float(np.abs(A_h).max()) > 2.0**20
+            res_h = A_h * (half if big else two)
+            K.copy_view(A_d * (0.5 if big else 2.0), pool_d[dst])
+        else:
+            res_h = A_h.copy()
+            K.copy_view(A_d, pool_d[dst])  # possibly a transposing copy onto itself's source
+        pool_h[dst] = np.ascontiguousarray(res_h)
+        if dst == a and tr_a:
+            # an in-place transposing copy reads what it overwrites: keep the
+            # pool well-defined by restoring the destination from the host
+            pool_d[dst] = dev(pool_h[dst])
+    d = _stats() - s0
+    for i, (h_, d_) in enumerate(zip(pool_h, pool_d)):
+        assert_bitexact(host(d_), h_, f"pool tensor {i}")
+    assert d[0] >= 20, d  # the stream did overlap independent kernels
