@@ -600,9 +600,10 @@ def bench_copy_reference(iters: int = 8) -> dict:
     """The library's own contiguous copy (the elementwise engine's flat
     kernel, nt_copy) on cold buffers: 4 pairs of 2^26 fp32 arrays (2 GB in
     all, far beyond the 256 MB Infinity Cache) used in turn, launches back
-    to back between two events.  The practical HBM rate of a read + write
-    stream on this GPU, against which the sweep's fraction of the published
-    peak reads."""
+    to back between two events (the four copies are independent, so the
+    launch window lets them overlap, as it does the sweep's kernels).  The
+    practical HBM rate of a read + write stream on this GPU, against which
+    the sweep's fraction of the published peak reads."""
     n = 1 << 26
     pairs = [(_fresh((n,)), _fresh((n,))) for _ in range(4)]
     K.copy_view(*pairs[-1])
@@ -623,8 +624,12 @@ def bench_copy_sweep_size(iters: int = 16) -> dict:
     (the bytes of one contiguous unary forward), contiguous and from a `.T`
     view of a [4096, 4096] array (the bytes and layout of a transposed
     unary forward), over 8 rotating pairs (1 GB, not Infinity-Cache
-    resident).  The ceiling a launch of that length reaches, ramp-up and
-    drain included, for the sweep's contiguous and transposed kernels."""
+    resident).  `ms` is timed as the sweep's per-kernel pass times its
+    kernels, events around each launch (every copy ordered after the one
+    before): the ceiling one launch of that length reaches, ramp-up and
+    drain included, for the per-kernel figures.  `back_to_back_ms` is the
+    same launches between two events only, where the independent copies
+    overlap in the launch window."""
     n = 1 << 24
     side = 1 << 12
     pairs = [(_fresh((side, side)), _fresh((side, side))) for _ in range(8)]
@@ -632,6 +637,13 @@ def bench_copy_sweep_size(iters: int = 16) -> dict:
     for name, src in (("contiguous", lambda a: a), ("transposed", lambda a: a.T)):
         for a, b in pairs:
             K.copy_view(src(a), b)
+        tm = Timer()
+        for it in range(iters):
+            a, b = pairs[it % 8]
+            tm.run(name, lambda a=a, b=b: K.copy_view(src(a), b))
+        nt.sync()
+        ds = tm.durations()[name]
+        ms = sum(ds) / len(ds)
         e0, e1 = _lib.Event(), _lib.Event()
         e0.record()
         for it in range(iters):
@@ -639,10 +651,12 @@ def bench_copy_sweep_size(iters: int = 16) -> dict:
             K.copy_view(src(a), b)
         e1.record()
         nt.sync()
-        ms = e0.elapsed_ms(e1) / iters
+        b2b = e0.elapsed_ms(e1) / iters
         gbs = 8 * n / (ms * 1e-3) / 1e9
         out[name] = {"ms": round(ms, 5), "GB/s": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": 8 * n}
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": 8 * n,
+                     "back_to_back_ms": round(b2b, 5),
+                     "back_to_back_frac": round(8 * n / (b2b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     return out
 
 

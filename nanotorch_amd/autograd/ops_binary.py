@@ -250,8 +250,9 @@ class LinearOp(Function):
     MatmulOp then an AddOp (src/nanotorch/nn/module.py:73-75), with the same
     two fp32 roundings (the product's, then the add's).  Its backward is
     those two ops' backward: dx = g . W^T and dW = x^T . g (MatmulOp,
-    ops_binary.py:253-267, each one product reading the transposed operand
-    in place), db = g summed over the rows (AddOp's unbroadcast, :49-50)."""
+    src/nanotorch/autograd/ops_binary.py:253-267, each one product reading
+    the transposed operand in place), db = g summed over the rows (AddOp's
+    unbroadcast, same file :49-50)."""
 
     def forward(self, x: Tensor, W: Tensor, b: Tensor) -> Tensor:
         self.save_for_backward(x, W)
