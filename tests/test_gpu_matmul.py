@@ -246,3 +246,56 @@ def test_linear_fused_forward_and_backward_match_the_composition(gpu):
         results.append([host(z), host(X.grad), host(W.grad), host(b.grad)])
     for name, f, c in zip(("z", "dx", "dW", "db"), *results):
         assert_bitexact(f, c, name)
+
+
+@pytest.mark.parametrize("x_T", [False, True])
+@pytest.mark.parametrize("x_grad,W_grad,b_grad", [(True, True, True), (False, True, True),
+                                                  (True, False, False), (False, False, True)])
+def test_linear_fused_grad_subsets_and_views(gpu, x_T, x_grad, W_grad, b_grad):
+    """LinearOp against x @ W + b with the input read through a `.T` view
+    and with each subset of x, W and b requiring a gradient (a frozen
+    layer, the first layer's input): every gradient that exists matches
+    the composition's bit for bit, the others stay None, and under no_grad
+    neither form records a graph."""
+    from nanotorch_amd import nn
+    r = rng(seed_of("linear-subsets", x_T, x_grad, W_grad, b_grad))
+    x = r.standard_normal((300, 130)).astype(np.float32)
+    g = r.standard_normal((300, 96)).astype(np.float32)
+    W0 = (r.standard_normal((130, 96)) / np.sqrt(130)).astype(np.float32)
+    b0 = r.standard_normal(96).astype(np.float32)
+    lin = nn.Linear(130, 96)
+    results = []
+    for fused in (True, False):
+        W, b = dev(W0, requires_grad=W_grad), dev(b0, requires_grad=b_grad)
+        leaf = dev(np.ascontiguousarray(x.T), requires_grad=x_grad) if x_T else dev(x, requires_grad=x_grad)
+        X = leaf.T if x_T else leaf
+        if fused:
+            lin._W, lin._b = W, b
+            z = lin(X)
+            assert type(z.grad_fn).__name__ == "LinearOp"
+        else:
+            z = X @ W + b
+        (z * dev(g)).sum().backward()
+        results.append([host(z)] + [None if t.grad is None else host(t.grad) for t in (leaf, W, b)])
+        with nt.no_grad():
+            lin._W, lin._b = W, b
+            assert (lin(X) if fused else X @ W + b).grad_fn is None
+    for name, f, c, need in zip(("z", "dx", "dW", "db"), *results, (True, x_grad, W_grad, b_grad)):
+        if not need:
+            assert f is None and c is None, name
+        else:
+            assert_bitexact(f, c, name)
+
+
+def test_linear_fused_saved_input_modified_in_place_raises(gpu):
+    """LinearOp saves x and W for its backward: an in-place change to the
+    input after the forward invalidates the saved version, and backward
+    raises as it does for MatmulOp."""
+    from nanotorch_amd import nn
+    lin = nn.Linear(8, 4)
+    h = dev(np.ones((5, 8), np.float32), requires_grad=True) * 2.0  # a non-leaf input
+    z = lin(h)
+    assert type(z.grad_fn).__name__ == "LinearOp"
+    h += 1.0
+    with pytest.raises(RuntimeError):
+        z.sum().backward()
