@@ -112,17 +112,21 @@ N_ELEM = 4096 * 4096
 
 def ew_bytes(name: str, phase: str) -> int:
     """Algorithmic bytes per launch (fp32, 2^24 elements): each distinct
-    tensor read once, each output written once.  Backward is accumulate
-    mode: reads g (+ saved inputs) + old grads, writes the grads."""
+    tensor read once, each output written once.  `bwd` is accumulate mode:
+    reads g (+ saved inputs) + old grads, writes the grads; `bwd_first` is
+    first-write mode: reads g (+ saved inputs), writes the grads (add and
+    sub write both, as the kernel does when handed both outputs)."""
     per = {
         ("fwd", "bin"): 12, ("fwd", "un"): 8,
         ("bwd", "add"): 20, ("bwd", "sub"): 20, ("bwd", "mul"): 28, ("bwd", "truediv"): 28,
         ("bwd", "neg"): 12,
+        ("bwd_first", "add"): 12, ("bwd_first", "sub"): 12, ("bwd_first", "mul"): 20,
+        ("bwd_first", "truediv"): 20, ("bwd_first", "neg"): 8,
     }
     binary = name in ("add", "sub", "mul", "truediv")
     if phase == "fwd":
         return per[("fwd", "bin" if binary else "un")] * N_ELEM
-    return per.get(("bwd", name), 16) * N_ELEM
+    return per.get((phase, name), 16 if phase == "bwd" else 12) * N_ELEM
 
 
 class ElementwiseSweep:
@@ -143,12 +147,15 @@ class ElementwiseSweep:
         r = np.random.default_rng(seed)
         shape = (4096, 4096)
         self.calls: list[tuple[str, str, str, object]] = []  # (op, layout, phase, fn)
+        # the same backwards in first-write mode (not part of the step)
+        self.first_write_calls: list[tuple[str, str, str, object]] = []
         lib = _lib.load()
         keep = []  # keep tensors alive
         for layout in ("contig", "transposed"):
             mk = dev if layout == "contig" else dev_T
             fwds: list = []
             bwds: list = []
+            firsts: list = []
             for name, op in BINARY_OPS:
                 a = r.standard_normal(shape).astype(np.float32)
                 b = (r.uniform(0.5, 2, shape) if name == "truediv" else r.standard_normal(shape)).astype(np.float32)
@@ -160,9 +167,10 @@ class ElementwiseSweep:
                 va, vb, vg, vo, vga, vgb = view(ta), view(tb), view(tg), view(out), view(ga), view(gb)
                 keep += [ta, tb, tg, out, ga, gb, va, vb, vg, vo, vga, vgb]
                 fwds.append((name, layout, "fwd", (lib.nt_binary, (op, ctypes.byref(va), ctypes.byref(vb), ctypes.byref(vo)))))
-                bwds.append((name, layout, "bwd", (lib.nt_binary_bwd, (
-                    op, ctypes.byref(vg), ctypes.byref(va), ctypes.byref(vb),
-                    ctypes.byref(vga), 1, ctypes.byref(vgb), 1))))
+                for acc, lst in ((1, bwds), (0, firsts)):
+                    lst.append((name, layout, "bwd" if acc else "bwd_first", (lib.nt_binary_bwd, (
+                        op, ctypes.byref(vg), ctypes.byref(va), ctypes.byref(vb),
+                        ctypes.byref(vga), acc, ctypes.byref(vgb), acc))))
             for name, op, dom, saved, e in UNARY_OPS:
                 x = (r.standard_normal(shape) if dom is None else r.uniform(dom[0], dom[1], shape)).astype(np.float32)
                 g = r.standard_normal(shape).astype(np.float32)
@@ -174,15 +182,18 @@ class ElementwiseSweep:
                 vs = vo if saved == "out" else (vx if saved == "in" else None)
                 keep += [tx, tg, out, gx, vx, vg, vo, vgx]
                 fwds.append((name, layout, "fwd", (lib.nt_unary, (op, ctypes.byref(vx), e, ctypes.byref(vo)))))
-                bwds.append((name, layout, "bwd", (lib.nt_unary_bwd, (
-                    op, ctypes.byref(vg), ctypes.byref(vs) if vs is not None else None, e,
-                    ctypes.byref(vgx), 1))))
+                for acc, lst in ((1, bwds), (0, firsts)):
+                    lst.append((name, layout, "bwd" if acc else "bwd_first", (lib.nt_unary_bwd, (
+                        op, ctypes.byref(vg), ctypes.byref(vs) if vs is not None else None, e,
+                        ctypes.byref(vgx), acc))))
             self.calls += fwds + bwds
+            self.first_write_calls += firsts
         self._keep = keep
         self.step_bytes = sum(ew_bytes(n, ph) for n, _, ph, _ in self.calls)
 
-    def step(self, timer: Timer | None = None) -> None:
-        for name, layout, phase, (fn, args) in self.calls:
+    def step(self, timer: Timer | None = None, first_write: bool = False) -> None:
+        for name, layout, phase, (fn, args) in (self.first_write_calls if first_write
+                                                 else self.calls):
             if timer is None:
                 _lib.check(fn(*args))
             else:
@@ -197,12 +208,14 @@ def launch_stats() -> dict:
     return {"unordered": u.value, "ordered": o.value, "fences": f.value}
 
 
-def bench_elementwise(steps: int, warmup: int) -> dict:
+def bench_elementwise(steps: int, warmup: int, first_write: bool = False) -> dict:
     """The sweep's whole-step time (events around the K steps; independent
     kernels overlap where the library's launch window admits them), then a
     per-kernel pass with events around each launch, which orders every
     kernel after the one before (no overlap): the per-kernel figures and the
-    roofline come from that pass."""
+    roofline come from that pass.  With `first_write`, the 24 backwards
+    again in first-write mode (the grads overwritten, not accumulated),
+    timed per launch the same way; not part of the step."""
     sw = ElementwiseSweep()
     for _ in range(warmup):
         sw.step()
@@ -231,9 +244,22 @@ def bench_elementwise(steps: int, warmup: int) -> dict:
         per[key] = {"ms": round(avg, 5), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                     "bytes": ew_bytes(name, phase)}
     launches = {k: (l1[k] - l0[k]) / steps for k in l0}
+    # the 24 backwards in first-write mode, timed the same way (per launch)
+    tf = Timer()
+    for _ in range(max(2, steps // 2) if first_write else 0):
+        sw.step(tf, first_write=True)
+    nt.sync()
+    first = {}
+    for key, ds in tf.durations().items():
+        name, layout, phase = key.split("|")
+        avg = sum(ds) / len(ds)
+        gbs = ew_bytes(name, phase) / (avg * 1e-3) / 1e9
+        first[key] = {"ms": round(avg, 5), "GB/s": round(gbs, 1),
+                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": ew_bytes(name, phase)}
     return {"ms_per_step": total_ms / steps, "step_bytes": sw.step_bytes, "per_kernel": per,
             "launches_per_step": launches,
-            "sum_of_kernel_ms": round(sum(v["ms"] for v in per.values()), 5)}
+            "sum_of_kernel_ms": round(sum(v["ms"] for v in per.values()), 5),
+            "first_write": first}
 
 
 # ---------------------------------------------------- config 3: reductions
@@ -1403,7 +1429,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--parts", default="all",
-                    help="all | none (the headline sweep only) | comma list of ew,red,mm,mlp,next,cpu")
+                    help="all | none (the headline sweep only) | comma list of "
+                         "ew,first,red,mm,mlp,next,cpu (first: the sweep's backwards in "
+                         "first-write mode)")
     ap.add_argument("--mlp-steps", type=int, default=20)
     ap.add_argument("--calib", action="store_true",
                     help="first run 3 plain copies of 2^24 fp32 (64 MiB read + 64 MiB "
@@ -1424,7 +1452,7 @@ def main() -> int:
     if not nt.is_available():
         print("no HIP device / libnt.so", file=sys.stderr)
         return 1
-    parts = {"ew", "red", "mm", "mlp", "next", "cpu"} if args.parts == "all" else (
+    parts = {"ew", "first", "red", "mm", "mlp", "next", "cpu"} if args.parts == "all" else (
         {"ew"} if args.parts == "none" else set(args.parts.split(",")))
 
     if args.calib:
@@ -1448,7 +1476,7 @@ def main() -> int:
         print(json.dumps(line), flush=True)
         return 0
 
-    ew = bench_elementwise(args.steps, args.warmup)
+    ew = bench_elementwise(args.steps, args.warmup, first_write="first" in parts)
     value = ew["step_bytes"] / (ew["ms_per_step"] * 1e-3) / 1e9
     # dominant kernel: the one with the largest share of the sweep's time
     dom_key, dom = max(ew["per_kernel"].items(), key=lambda kv: kv[1]["ms"])
@@ -1486,6 +1514,14 @@ def main() -> int:
         "sum_of_kernel_ms": ew["sum_of_kernel_ms"],
         "parts": {"elementwise_per_kernel": ew["per_kernel"]},
     }
+    if ew["first_write"]:
+        fw = ew["first_write"]
+        fb = sum(v["bytes"] for v in fw.values())
+        fms = sum(v["ms"] for v in fw.values())
+        line["parts"]["elementwise_first_write"] = {
+            "per_kernel": fw,
+            "aggregate_GB/s": round(fb / (fms * 1e-3) / 1e9, 1),
+            "aggregate_frac": round(fb / (fms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     copy_ref = bench_copy_reference()
     copy_ref["sweep_vs_copy"] = round(value / copy_ref["GB/s"], 4)
     line["parts"]["copy_reference"] = copy_ref

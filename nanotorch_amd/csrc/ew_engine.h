@@ -1117,8 +1117,11 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
       //    heavy functors, whose two resident workgroups per CU then wait on
       //    each other's compute (tanh / sigmoid forwards 10% slower): they
       //    keep 64 x 128;
-      //  * two exchanged streams (the backward of an op with a saved output,
-      //    exchanging its `.T` gradient in and out): 64 x 128;
+      //  * two exchanged outputs and no exchanged input (an add / sub
+      //    backward writing two `.T` gradients): 128 x 128 (36 us against
+      //    40 us in 64 x 128);
+      //  * two exchanged streams otherwise (the backward of an op with a
+      //    saved output, exchanging its `.T` gradient in and out): 64 x 128;
       //  * more: 64 x 64.
       // Whole sweep 2% faster than the previous 128 x 64 / 64 x 128 / 64 x 64
       // rule.
@@ -1135,7 +1138,7 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
           return tile4.template operator()<32, 256>();
         if (n_col == 1 && n_row >= 3)
           return tile4.template operator()<32, 256>();
-        if (n_col == 1 && !ew_heavy<F>())
+        if ((n_col == 1 || (n_col == 2 && col_in == 0)) && !ew_heavy<F>())
           return tile4.template operator()<128, 128>();
         if (n_col <= 2)
           return tile4.template operator()<64, 128>();
