@@ -521,13 +521,15 @@ def _index_args(fn: str, plan, first, second, keep_alive: list) -> list:
 
 
 def bench_next(iters: int = 12) -> dict:
-    """The rows next to the hot path, each timed per launch with HIP events
-    on the library stream: device casts and a comparison (no host round
-    trip), strided copies of a transposed 2-D view and of a batch of
-    transposed planes, a batched matmul on the MFMA
-    kernel, and advanced-index gather / scatter of rows.  Bytes are
-    algorithmic (every operand once); GB/s against the HBM peak, TFLOP/s
-    against the fp32 MFMA peak."""
+    """The rows next to the hot path, each timed over `iters` launches back
+    to back between two HIP events on the library stream (elementwise
+    launches on the rotating operand sets are independent and may overlap
+    in the launch window): device casts and a comparison (no host round
+    trip), strided copies of a transposed 2-D view and of batches of
+    transposed planes, a batched matmul on the MFMA kernel, and
+    advanced-index gather / scatter of rows.  Bytes are algorithmic (every
+    operand once); GB/s against the HBM peak, TFLOP/s against the fp32 MFMA
+    peak."""
     from nanotorch_amd import _fancy
     import ctypes
     r = np.random.default_rng(6)
@@ -572,6 +574,12 @@ def bench_next(iters: int = 12) -> dict:
     gbytes = 2 * gouts[0].numel * 4 + 8 * len(ids)
     a3 = [t.reshape(64, 1024, 1024) for t in a]
     o3 = [t.reshape(64, 1024, 1024) for t in o32]
+    # [64, 512, 512] transposed two ways: 64 planes of 512 x 512 (axes 1, 2),
+    # and 512 planes of 512 x 64 (axes 0, 2)
+    p3 = copies(dev(r.standard_normal((64, 512, 512)).astype(np.float32)))
+    q3 = [_fresh((64, 512, 512)) for _ in range(SETS)]
+    q3r = [_fresh((512, 512, 64)) for _ in range(SETS)]
+    n4 = 64 * 512 * 512
     cases = {
         # name: (launch of set k, bytes or None, flop or None)
         "cast|f32->f64": (lambda k: K.copy_view(a[k], o64[k]), 12 * n, None),
@@ -581,6 +589,10 @@ def bench_next(iters: int = 12) -> dict:
         "copy|transposed": (lambda k: K.copy_view(a[k].T, o32[k]), 8 * n, None),
         # a batch of 64 planes: [64, 1024, 1024].transpose(1, 2) -> contiguous
         "copy|3-D transpose(1,2)": (lambda k: K.copy_view(a3[k].transpose(1, 2), o3[k]), 8 * n, None),
+        "copy|[64,512,512].transpose(1,2)": (lambda k: K.copy_view(p3[k].transpose(1, 2), q3[k]),
+                                             8 * n4, None),
+        "copy|[64,512,512].transpose(0,2)": (lambda k: K.copy_view(p3[k].transpose(0, 2), q3r[k]),
+                                             8 * n4, None),
         "matmul|batched 16x1024^3": (lambda k: K.matmul_into(xb, yb, ob3, accumulate=False),
                                      None, 2 * B * Mb**3),
         "gather|8192 rows of [50000,1024]": (lambda k: _lib.call("nt_gather_axes", *gargs[k]),
