@@ -520,7 +520,33 @@ def _index_args(fn: str, plan, first, second, keep_alive: list) -> list:
     return args
 
 
-def bench_next(iters: int = 12) -> dict:
+_N8K = 8192 * 8192
+_N4 = 64 * 512 * 512
+# bench_next's cases in queue order: name, a substring of the kernel each
+# call launches, kernels per call, algorithmic bytes (or None), FLOP (or
+# None).  Every case runs 1 + NEXT_ITERS calls (an untimed first call).
+NEXT_ROWS = [
+    ("cast|f32->f64", "CastOp<float, double>", 1, 12 * _N8K, None),
+    ("cast|f64->f32", "CastOp<double, float>", 1, 12 * _N8K, None),
+    ("cast|i64->f32", "CastOp<long, float>", 1, 12 * _N8K, None),
+    ("compare|gt", "CompareFwd", 1, 9 * _N8K, None),
+    ("copy|transposed", "ew_tile4_kernel", 1, 8 * _N8K, None),
+    # a batch of 64 planes: [64, 1024, 1024].transpose(1, 2) -> contiguous
+    ("copy|3-D transpose(1,2)", "ew_tile4_kernel", 1, 8 * _N8K, None),
+    # [64, 512, 512] transposed two ways: 64 planes of 512 x 512 (axes 1, 2),
+    # and 512 planes of 512 x 64 (axes 0, 2)
+    ("copy|[64,512,512].transpose(1,2)", "ew_tile4_kernel", 1, 8 * _N4, None),
+    ("copy|[64,512,512].transpose(0,2)", "ew_tile4_kernel", 1, 8 * _N4, None),
+    ("matmul|batched 16x1024^3", "mm_f32_mfma", 1, None, 2 * 16 * 1024**3),
+    ("gather|8192 rows of [50000,1024]", "row_index_kernel", 1, 2 * 8192 * 1024 * 4 + 8 * 8192, None),
+    ("scatter|8192 rows of [50000,1024]", "row_index_kernel", 1, 2 * 8192 * 1024 * 4 + 8 * 8192, None),
+    # the reference's generator stream drawn on the device: bytes written
+    ("uniform|f32 [8192,8192]", "rng_", 4, 4 * _N8K, None),
+]
+NEXT_ITERS = 12
+
+
+def bench_next(iters: int = NEXT_ITERS) -> dict:
     """The rows next to the hot path, each timed over `iters` launches back
     to back between two HIP events on the library stream (elementwise
     launches on the rotating operand sets are independent and may overlap
@@ -574,36 +600,26 @@ def bench_next(iters: int = 12) -> dict:
     gbytes = 2 * gouts[0].numel * 4 + 8 * len(ids)
     a3 = [t.reshape(64, 1024, 1024) for t in a]
     o3 = [t.reshape(64, 1024, 1024) for t in o32]
-    # [64, 512, 512] transposed two ways: 64 planes of 512 x 512 (axes 1, 2),
-    # and 512 planes of 512 x 64 (axes 0, 2)
     p3 = copies(dev(r.standard_normal((64, 512, 512)).astype(np.float32)))
     q3 = [_fresh((64, 512, 512)) for _ in range(SETS)]
     q3r = [_fresh((512, 512, 64)) for _ in range(SETS)]
-    n4 = 64 * 512 * 512
-    cases = {
-        # name: (launch of set k, bytes or None, flop or None)
-        "cast|f32->f64": (lambda k: K.copy_view(a[k], o64[k]), 12 * n, None),
-        "cast|f64->f32": (lambda k: K.copy_view(a64[k], o32[k]), 12 * n, None),
-        "cast|i64->f32": (lambda k: K.copy_view(lab[k], o32[k]), 12 * n, None),
-        "compare|gt": (lambda k: _lib.call("nt_binary", *cmp_args[k]), 9 * n, None),
-        "copy|transposed": (lambda k: K.copy_view(a[k].T, o32[k]), 8 * n, None),
-        # a batch of 64 planes: [64, 1024, 1024].transpose(1, 2) -> contiguous
-        "copy|3-D transpose(1,2)": (lambda k: K.copy_view(a3[k].transpose(1, 2), o3[k]), 8 * n, None),
-        "copy|[64,512,512].transpose(1,2)": (lambda k: K.copy_view(p3[k].transpose(1, 2), q3[k]),
-                                             8 * n4, None),
-        "copy|[64,512,512].transpose(0,2)": (lambda k: K.copy_view(p3[k].transpose(0, 2), q3r[k]),
-                                             8 * n4, None),
-        "matmul|batched 16x1024^3": (lambda k: K.matmul_into(xb, yb, ob3, accumulate=False),
-                                     None, 2 * B * Mb**3),
-        "gather|8192 rows of [50000,1024]": (lambda k: _lib.call("nt_gather_axes", *gargs[k]),
-                                             gbytes, None),
-        "scatter|8192 rows of [50000,1024]": (lambda k: _lib.call("nt_scatter_axes", *sargs[k]),
-                                              gbytes, None),
-        # the reference's generator stream drawn on the device: bytes written
-        "uniform|f32 [8192,8192]": (lambda k: _lib.call("nt_device_uniform", o32[k]._storage.data_ptr(),
-                                                        int(nt.float32), n, 0.0, 1.0),
-                                    4 * n, None),
+    launch = {
+        "cast|f32->f64": lambda k: K.copy_view(a[k], o64[k]),
+        "cast|f64->f32": lambda k: K.copy_view(a64[k], o32[k]),
+        "cast|i64->f32": lambda k: K.copy_view(lab[k], o32[k]),
+        "compare|gt": lambda k: _lib.call("nt_binary", *cmp_args[k]),
+        "copy|transposed": lambda k: K.copy_view(a[k].T, o32[k]),
+        "copy|3-D transpose(1,2)": lambda k: K.copy_view(a3[k].transpose(1, 2), o3[k]),
+        "copy|[64,512,512].transpose(1,2)": lambda k: K.copy_view(p3[k].transpose(1, 2), q3[k]),
+        "copy|[64,512,512].transpose(0,2)": lambda k: K.copy_view(p3[k].transpose(0, 2), q3r[k]),
+        "matmul|batched 16x1024^3": lambda k: K.matmul_into(xb, yb, ob3, accumulate=False),
+        "gather|8192 rows of [50000,1024]": lambda k: _lib.call("nt_gather_axes", *gargs[k]),
+        "scatter|8192 rows of [50000,1024]": lambda k: _lib.call("nt_scatter_axes", *sargs[k]),
+        "uniform|f32 [8192,8192]": lambda k: _lib.call(
+            "nt_device_uniform", o32[k]._storage.data_ptr(), int(nt.float32), n, 0.0, 1.0),
     }
+    assert list(launch) == [c[0] for c in NEXT_ROWS] and gbytes == NEXT_ROWS[9][3]
+    cases = {name: (launch[name], nbytes, flop) for name, _, _, nbytes, flop in NEXT_ROWS}
     out = {}
     for name, (fn, nbytes, flop) in cases.items():
         # back-to-back launches of one case between two events: the average
@@ -1010,6 +1026,11 @@ def _short(name: str) -> str:
     return n.replace("void nt::", "").replace("nt::", "")
 
 
+def _mdc(v) -> str:
+    """A markdown table cell: `|` inside a key (e.g. add|contig|fwd) escaped."""
+    return str(v).replace("|", "\\|")
+
+
 def _sweep_key(name: str):
     """Kernel name -> 'op|layout|phase' of the sweep (flat kernel: contiguous
     operands; tile kernel: transposed views)."""
@@ -1088,9 +1109,56 @@ def _summarize_sweep_trace(path: str, out_md: str) -> None:
                 "min us | max us | share of kernel time % |\n|---|---|---|---|---|---|---|---|---|\n")
         for (name, sk, grid), v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
             tp = v[-SWEEP_TIMER_SWEEPS:] if sk else v
-            o.write(f"| `{name[:150]}` | {sk} | {grid} | {len(v)} | {sum(v) / len(v):.2f} | "
+            o.write(f"| `{name[:150]}` | {_mdc(sk)} | {grid} | {len(v)} | {sum(v) / len(v):.2f} | "
                     f"{sum(tp) / len(tp):.2f} | {min(v):.2f} | {max(v):.2f} | "
                     f"{100 * sum(v) / total:.2f} |\n")
+
+
+def _summarize_next_trace(path: str, out_md: str) -> None:
+    """Next-row kernel times per bench_next case from the kernel trace: the
+    dispatches from the first case's kernel on are assigned to the cases in
+    queue order (NEXT_ROWS: 1 + NEXT_ITERS calls each, its kernels per call;
+    the library's barrier kernels and the runtime's copy kernels left out),
+    each case's first call untimed as in bench_next.  Several cases share a
+    kernel (and a grid size), so a per-kernel table cannot tell them apart."""
+    import csv
+    rows = sorted(csv.DictReader(open(os.path.join(path, "run_kernel_trace.csv"))),
+                  key=lambda r: int(r["Dispatch_Id"]))
+    # neither the barrier kernels nor the runtime's copy kernels (the first
+    # device draw uploads the generator's tables) belong to a case's calls
+    rows = [r for r in rows if "stream_fence_kernel" not in r["Kernel_Name"]
+            and "__amd_rocclr" not in r["Kernel_Name"]]
+    i = next(j for j, r in enumerate(rows) if NEXT_ROWS[0][1] in r["Kernel_Name"])
+    lines = []
+    for name, pat, per_call, nbytes, flop in NEXT_ROWS:
+        us, kname = [], ""
+        for c in range(1 + NEXT_ITERS):
+            ks = rows[i:i + per_call]
+            i += per_call
+            if len(ks) < per_call or not all(pat in r["Kernel_Name"] for r in ks):
+                raise SystemExit(f"next-row trace: the dispatches at {i - per_call} are not {name}")
+            kname = " + ".join(_short(r["Kernel_Name"])[:90] for r in ks)
+            if c:
+                us.append(sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in ks) / 1e3)
+        avg = sum(us) / len(us)
+        if flop is not None:
+            rate = f"{flop / (avg * 1e-6) / 1e12:.1f} TFLOP/s | {flop / (avg * 1e-6) / 1e12 / FP32_MFMA_PEAK_TFLOPS:.3f}"
+        else:
+            rate = f"{nbytes / (avg * 1e-6) / 1e9:.1f} GB/s | {nbytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS:.3f}"
+        lines.append(f"| {_mdc(name)} | `{kname}` | {len(us)} | {avg:.2f} | {min(us):.2f} | {max(us):.2f} | {rate} |")
+    with open(out_md, "w") as o:
+        o.write(f"# {PROFILE_FILES['next'][1]}\n\nCommand (repo root on the GPU box):\n\n"
+                f"```\n{PROFILE_CMDS['next']}\n```\n\n"
+                "Summarised with `python bench.py --summarize next gpurun_out/prof_next` from the "
+                "kernel trace: each case's dispatches, in queue order, its first call untimed as in "
+                "bench.py.  `us` is the kernel time per call (the uniform draw: its four kernels "
+                "summed); the rate is the case's algorithmic bytes (or FLOP) over it, against "
+                f"{HBM_PEAK_GBS / 1000:.0f} TB/s (or {FP32_MFMA_PEAK_TFLOPS} TFLOP/s).  bench.py's own "
+                "figures time the same calls back to back between two events, where independent "
+                "elementwise launches over the rotating operand sets may overlap.\n\n"
+                "| case | kernel(s) | timed calls | avg us | min us | max us | rate | frac |\n"
+                "|---|---|---|---|---|---|---|---|\n")
+        o.write("\n".join(lines) + "\n")
 
 
 def _summarize_mm_trace(path: str, out_md: str) -> None:
@@ -1219,7 +1287,8 @@ def _summarize_pmc(part: str, dirs: list[str], out_md: str, title: str, keep) ->
     with open(out_md, "w") as o:
         o.write(f"# {title}\n\nCommands (repo root on the GPU box):\n\n```\n"
                 f"{PROFILE_CMDS[part + '_pmc1']}\n{PROFILE_CMDS[part + '_pmc2']}\n```\n\n"
-                f"Summarised with `python bench.py --summarize {part}_pmc gpurun_out/prof_{part}_pmc1 "
+                f"Summarised with `python bench.py --summarize {'mm_pmc12' if part == 'mm' else part + '_pmc'} "
+                f"gpurun_out/prof_{part}_pmc1 "
                 f"gpurun_out/prof_{part}_pmc2`.  Per dispatch, averaged; durations from the first "
                 "(counter-collecting) pass.  SQ cycle counters are summed over the GPU's waves in "
                 "units of 4 cycles (so resident waves per CU = 4 x SQ_WAVE_CYCLES / (256 CUs x "
@@ -1237,7 +1306,7 @@ def _summarize_pmc(part: str, dirs: list[str], out_md: str, title: str, keep) ->
                 "VALU busy | VALU/wave | bank-conflict | VMEM level/inst |\n"
                 "|---|---|---|---|---|---|---|---|---|---|---|---|\n")
         for r in rows:
-            o.write(f"| `{r[0][:110]}` | {r[1]} | {r[2]} | {r[3]:.1f} | {r[4]:.1f} | {r[5]:.2f} | "
+            o.write(f"| `{r[0][:110]}` | {_mdc(r[1])} | {r[2]} | {r[3]:.1f} | {r[4]:.1f} | {r[5]:.2f} | "
                     f"{r[6]:.2f} | {r[7]:.3f} | {r[8]:.2f} | {r[9]:.0f} | {r[10]:.3f} | {r[11]:.0f} |\n")
 
 
@@ -1267,7 +1336,7 @@ def _summarize_bytes(part: str, dirs: list[str], out_md: str, title: str, expect
             wr_ = w.get(key, {}).get("WRITE_SIZE", 0.0) * ws / 1024
             if rd + wr_ < 1.0:
                 continue
-            o.write(f"| `{key[0][:110]}` | {key[1]} | {int(f[key]['dispatches'])} | {rd:.1f} | "
+            o.write(f"| `{key[0][:110]}` | {_mdc(key[1])} | {int(f[key]['dispatches'])} | {rd:.1f} | "
                     f"{wr_:.1f} | {expect(key[0], key[1]) or ''} |\n")
 
 
@@ -1325,7 +1394,7 @@ def _summarize_tile_variants(base: str, out_md: str) -> None:
                 "| kernel | variant | tile | us | frac | waves/CU | wait | issue-wait | VALU busy | "
                 "bank-conflict |\n|---|---|---|---|---|---|---|---|---|---|\n")
         for key, lbl, tile, us, wv, w, iw, vb, bc in sorted(rows, key=lambda r: (r[0], r[3])):
-            o.write(f"| {key} | {lbl} | {tile} | {us:.1f} | {nb[key] / (us * 1e-6) / 8e12:.3f} | "
+            o.write(f"| {_mdc(key)} | {lbl} | {tile} | {us:.1f} | {nb[key] / (us * 1e-6) / 8e12:.3f} | "
                     f"{wv:.1f} | {w:.2f} | {iw:.2f} | {vb:.2f} | {bc:.3f} |\n")
 
 
@@ -1364,6 +1433,9 @@ def summarize(kind: str, dirs: list[str]) -> None:
     if kind == "mm":
         _summarize_mm_trace(dirs[0], os.path.join(prof, PROFILE_FILES["mm"][0]))
         return
+    if kind == "next":
+        _summarize_next_trace(dirs[0], os.path.join(prof, PROFILE_FILES["next"][0]))
+        return
     if kind in PROFILE_FILES:
         fname, title = PROFILE_FILES[kind]
         rows = list(csv.DictReader(open(os.path.join(dirs[0], "run_kernel_stats.csv"))))
@@ -1375,7 +1447,7 @@ def summarize(kind: str, dirs: list[str]) -> None:
              "| kernel | sweep key | calls | avg us | min us | max us | total % |",
              "|---|---|---|---|---|---|---|"]
         for r in rows:
-            o.append(f"| `{_short(r['Name'])[:150]}` | {_sweep_key(r['Name']) or ''} | {r['Calls']} | "
+            o.append(f"| `{_short(r['Name'])[:150]}` | {_mdc(_sweep_key(r['Name']) or '')} | {r['Calls']} | "
                      f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
                      f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
         with open(os.path.join(prof, fname), "w") as f:
@@ -1429,7 +1501,7 @@ def summarize(kind: str, dirs: list[str]) -> None:
         o.write("| kernel | FETCH_SIZE MiB | WRITE_SIZE MiB | scaled traffic MiB | algorithmic MiB |\n"
                 "|---|---|---|---|---|\n")
         for kk, fv, wv, t, alg in sorted(rows):
-            o.write(f"| {kk} | {fv:.1f} | {wv:.1f} | {t:.1f} | {alg:.1f} |\n")
+            o.write(f"| {_mdc(kk)} | {fv:.1f} | {wv:.1f} | {t:.1f} | {alg:.1f} |\n")
 
 
 # -------------------------------------------------------------------- main

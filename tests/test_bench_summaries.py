@@ -99,3 +99,59 @@ def test_byte_summary_scales_by_the_copy(tmp_path, monkeypatch):
     assert len(rows) == 1  # the calibration copy itself is not listed
     cells = [c.strip() for c in rows[0].split("|")]
     assert cells[4:6] == ["256.0", "0.0"]  # a 256 MiB read-only reduction
+
+
+def test_next_rows_summary_assigns_dispatches_to_cases(tmp_path, monkeypatch):
+    # Several next-row cases share one kernel and grid size (the transposed
+    # copies), so the summary walks the trace in queue order: set-up copies
+    # first, barrier and runtime copy kernels interleaved, then each case's
+    # 1 + NEXT_ITERS calls (the uniform draw four kernels per call), the
+    # first call of each untimed.
+    path = tmp_path / "prof_next"
+    path.mkdir()
+    rows, t = [], 0
+
+    def emit(name, us):
+        nonlocal t
+        rows.append({"Dispatch_Id": len(rows), "Kernel_Name": name,
+                     "Start_Timestamp": t, "End_Timestamp": t + int(us * 1000)})
+        t += int(us * 1000) + 500
+
+    emit("void nt::ew_flat_kernel<float, float, 1, 1, 4, 1, true, nt::CastOp<float, float> >(...)", 5)
+    want = {}
+    for ci, (name, pat, per_call, _, _) in enumerate(bench.NEXT_ROWS):
+        for c in range(1 + bench.NEXT_ITERS):
+            if c == 3:
+                emit("void nt::stream_fence_kernel()", 2)
+            if ci == len(bench.NEXT_ROWS) - 1 and c == 0:
+                emit("__amd_rocclr_copyBuffer", 4)
+            for k in range(per_call):
+                # the untimed first call is slow; timed calls take 10 + case index us
+                emit(f"void nt::{pat}kernel_{k}(...)", 99.0 if c == 0 else 10.0 + ci)
+        want[name] = per_call * (10.0 + ci)
+    with open(path / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    (tmp_path / "profiles").mkdir()
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    bench.summarize("next", [str(path)])
+    text = open(tmp_path / "profiles" / "next_rows_trace.md").read()
+    got = {}
+    for line in text.splitlines():
+        if line.startswith("| ") and "`" in line:
+            cells = [c.strip() for c in line.replace("\\|", "/").split(" | ")]
+            got[cells[0].lstrip("| ").replace("/", "|")] = (int(cells[2]), float(cells[3]))
+    assert got == {n: (bench.NEXT_ITERS, us) for n, us in want.items()}
+    # a trace whose dispatches do not follow the cases is refused
+    rows[5]["Kernel_Name"] = "void nt::something_else(...)"
+    with open(path / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    try:
+        bench.summarize("next", [str(path)])
+    except SystemExit as e:
+        assert "not" in str(e)
+    else:
+        raise AssertionError("a mismatched trace was summarised")
