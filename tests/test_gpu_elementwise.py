@@ -310,6 +310,58 @@ def test_binary_backward_kernel(gpu, name, op, oop, need, acc):
             assert_bitexact(got, w, f"{name} grad {i}")
 
 
+@pytest.mark.parametrize("name,op,oop,chain,dom,saved", UNARY_BWD)
+def test_unary_backward_first_write_into_transposed_target(gpu, name, op, oop, chain, dom, saved):
+    """The C ABI's first-write mode into an existing strided gradient (the
+    accumulate flag 0 with a target): the `.T` target overwritten, a saved
+    input read through `.T` and a saved output contiguous, as the sweep's
+    transposed layout has them; full and partial tiles."""
+    import ctypes
+    r = rng(seed_of("fw-T", name))
+    shape = (260, 388)
+    x = _inputs(r, dom, shape)
+    g = r.standard_normal(shape).astype(np.float32)
+    e = 2.5 if name == "pow" else 0.0
+    s = None if saved == "none" else (x if saved == "in" else O.unary(oop, x, e))
+    want = chain(g, s)
+    sv = None if s is None else (dev_T(s) if saved == "in" else dev(s))
+    tgt = dev_T(r.standard_normal(shape).astype(np.float32))  # overwritten
+    tg = dev(g)  # every operand held for the call
+    _lib.call("nt_unary_bwd", op, ctypes.byref(K.view_of(tg)),
+              _lib.ref(None if sv is None else K.view_of(sv)), float(e),
+              ctypes.byref(K.view_of(tgt)), 0)
+    got = host(tgt)
+    if name in ("pow", "log", "sqrt", "tanh"):
+        scale = np.abs(want).astype(np.float64)
+        if name == "tanh":
+            scale = np.abs(g).astype(np.float64) * (1 + s.astype(np.float64) ** 2)
+        assert_rel(got, want, 1e-6, name, scale=scale)
+    else:
+        assert_bitexact(got, want, name)
+
+
+@pytest.mark.parametrize("name,op,oop", BINARY)
+def test_binary_backward_first_write_into_transposed_targets(gpu, name, op, oop):
+    """First-write into two existing `.T` gradients (both outputs exchanged,
+    the inputs `.T` views too), through the C ABI."""
+    import ctypes
+    r = rng(seed_of("fw-T-bin", name))
+    shape = (260, 388)
+    a = r.standard_normal(shape).astype(np.float32)
+    b = (r.uniform(0.5, 2, shape) if name == "div" else r.standard_normal(shape)).astype(np.float32)
+    g = r.standard_normal(shape).astype(np.float32)
+    ga_w, gb_w = O.bwd_binary(oop, g, a, b)
+    ta, tb = (dev_T(r.standard_normal(shape).astype(np.float32)) for _ in range(2))
+    ops = (dev(g), dev_T(a), dev_T(b), ta, tb)  # every operand held for the call
+    vs = [K.view_of(t) for t in ops]
+    _lib.call("nt_binary_bwd", op, *(ctypes.byref(v) for v in vs[:4]), 0, ctypes.byref(vs[4]), 0)
+    assert_bitexact(host(ta), ga_w, f"{name} grad a")
+    if name == "div":  # reference form: (-a) / b**2 * g
+        assert_rel(host(tb), gb_w, 1e-6, f"{name} grad b", scale=np.abs(gb_w).astype(np.float64))
+    else:
+        assert_bitexact(host(tb), gb_w, f"{name} grad b")
+
+
 @pytest.mark.parametrize("shape", [(196, 452), (452, 196), (68, 132), (132, 68),
                                    (4, 260), (260, 4), (132, 132)])
 def test_tile_shapes_partial_tiles(gpu, shape):
