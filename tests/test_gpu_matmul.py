@@ -299,3 +299,18 @@ def test_linear_fused_saved_input_modified_in_place_raises(gpu):
     h += 1.0
     with pytest.raises(RuntimeError):
         z.sum().backward()
+
+
+def test_matmul_bias_strided_operands(gpu):
+    """nt_matmul_bias with a bias read through a stride-2 slice, an A whose
+    rows repeat (a stride-0 expand) and a B read through `.T`, on the 128x128
+    and the wide kernels: bit-identical to the product, then the add."""
+    r = rng(seed_of("mmbias-strided"))
+    for M, K_, N in ((200, 96, 136), (512, 512, 512)):
+        row = r.standard_normal((1, K_)).astype(np.float32)
+        ta = dev(row).expand(M, K_)                       # every row the same
+        tb = dev_T((r.standard_normal((K_, N)) / np.sqrt(K_)).astype(np.float32))
+        tbias = dev(r.standard_normal(2 * N).astype(np.float32))[::2]
+        fused = host(nt.Tensor._new_contiguous(K.matmul_bias(ta, tb, tbias, (M, N)), (M, N)))
+        prod = nt.Tensor._new_contiguous(K.matmul(ta, tb, (M, N)), (M, N))
+        assert_bitexact(fused, host(prod + tbias), f"strided bias {M}x{K_}x{N}")
