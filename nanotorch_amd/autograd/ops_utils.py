@@ -35,9 +35,3 @@ def broadcast_axis(axis, x: Tensor) -> TensorShape:
     if any(ax < 0 or ax >= x.ndim for ax in axis):
         raise IndexError(f"Invalid axis: {axis}")
     return axis
-
-
-def needs_reduce(x_shape: TensorShape, out_shape: TensorShape) -> bool:
-    """True if the gradient of an input of x_shape must be summed from
-    out_shape (broadcasting happened)."""
-    return tuple(x_shape) != tuple(out_shape)

@@ -1216,11 +1216,4 @@ void launch_elementwise(const nt_view *const *ins, const nt_view *const *outs,
   NT_LAUNCH_CHECK();
 }
 
-// Validates that every view has the same shape as the first one.
-inline void require_views_same_shape(const nt_view *const *views, int n,
-                                     const char *fname) {
-  for (int k = 1; k < n; ++k)
-    require_same_shape(views[0], views[k], fname);
-}
-
 } // namespace nt
