@@ -966,7 +966,7 @@ PMC_SET2 = ("SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_INSTS_LDS SQ_INSTS_VMEM_RD SQ_
 _PROF = "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/{d} -o run -- python -u bench.py {a}"
 _PMC = "rocprofv3 --pmc {c} --output-format csv -d gpurun_out/{d} -o run -- python -u bench.py {a}"
 PROFILE_CMDS = {
-    "sweep": _PROF.format(d="prof_sweep", a="--steps 5 --warmup 2 --parts ew --calib"),
+    "sweep": _PROF.format(d="prof_sweep", a="--steps 5 --warmup 2 --parts ew,first --calib"),
     "red": _PROF.format(d="prof_red", a="--parts red"),
     "mm": _PROF.format(d="prof_mm", a="--parts mm"),
     "mlp": _PROF.format(d="prof_mlp", a="--parts mlp --mlp-steps 5"),
@@ -1033,15 +1033,26 @@ def _mdc(v) -> str:
 
 def _sweep_key(name: str):
     """Kernel name -> 'op|layout|phase' of the sweep (flat kernel: contiguous
-    operands; tile kernel: transposed views)."""
+    operands; tile kernel: transposed views).  A backward is `bwd` when it
+    accumulates into its gradients (UnaryBwd's ACC, BinaryBwd's AA / AB for
+    the gradients it produces), `bwd_first` when it overwrites them."""
     import re
     layout = "contig" if "ew_flat_kernel" in name else ("transposed" if "ew_tile4_kernel" in name else None)
-    m = re.search(r"(UnaryFwd|UnaryBwd|BinaryFwd|BinaryBwd)<(\d+)", name)
+    m = re.search(r"(UnaryFwd|UnaryBwd|BinaryFwd|BinaryBwd)<(\d+)((?:, [a-z0-9 ]+)*)>", name)
     if not layout or not m:
         return None
     kind, op = m.group(1), int(m.group(2))
     opn = (_UN if kind.startswith("Unary") else _BI)[op]
-    return f"{opn}|{layout}|{'fwd' if kind.endswith('Fwd') else 'bwd'}"
+    if kind.endswith("Fwd"):
+        return f"{opn}|{layout}|fwd"
+    flags = [a.strip() == "true" for a in m.group(3).split(",")[2:]]  # after OP, T
+    if kind == "UnaryBwd":
+        acc = flags[:1]
+    else:  # NA, NB, AA, AB: the accumulate flags of the produced gradients
+        acc = [flags[2 + i] for i in range(2) if flags[i]]
+    if all(acc):
+        return f"{opn}|{layout}|bwd"
+    return f"{opn}|{layout}|{'bwd_first' if not any(acc) else 'bwd_mixed'}"
 
 
 def _mm_calls():
@@ -1103,6 +1114,9 @@ def _summarize_sweep_trace(path: str, out_md: str) -> None:
                 f"pass` averages the last {SWEEP_TIMER_SWEEPS} dispatches, bench.py's per-kernel "
                 "pass, whose events order every launch after the one before: the durations the "
                 "bench line's per-kernel figures and roofline are measured on.  "
+                "`bwd_first` rows are bench.py's first-write pass (part `first`: the same "
+                "backwards overwriting their gradients, events around each launch; every dispatch "
+                "of theirs belongs to that pass).  "
                 "`stream_fence_kernel` is the empty barrier kernel queued before an event or a "
                 "copy while overlapped kernels may still run.\n\n"
                 "| kernel | sweep key | grid | calls | all avg us | per-kernel pass avg us | "
